@@ -1,0 +1,190 @@
+// Error reporting, version, and the whole-layer driver moeq_moe_forward.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+extern "C" int moeq_gemm_tile_n(int bm, int epilogue);
+
+namespace moeq {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MOEQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MOEQ_OK;
+}
+
+// Launch plan of one layer forward; a pure function of (layer, T) so the
+// workspace query and the forward agree.
+struct Plan {
+  int bm, splits, max_tiles, y_dtype;
+  int64_t T, pairs, rows;
+  size_t off_idx, off_w, off_counts, off_offsets, off_row_token, off_row_pair, off_inv,
+      off_tiles, off_ntiles, off_perm, off_h, off_y, total;
+};
+
+static Plan make_plan(const moeq_moe *m, int64_t T) {
+  Plan p{};
+  p.T = T;
+  p.pairs = T * m->top_k;
+  p.rows = p.pairs + int64_t(m->n_shared) * T;
+  const double avg = double(p.pairs) / double(m->n_experts);
+  p.bm = avg <= 16 ? 16 : avg <= 32 ? 32 : avg <= 64 ? 64 : 128;
+  p.max_tiles = moeq_max_tiles(T, m->top_k, m->n_experts, m->n_shared, p.bm);
+  // Down projection: few live blocks (decode) -> split K over fp32 slices.
+  p.splits = 1;
+  if (p.bm == 16) {
+    const int64_t bn = moeq_gemm_tile_n(16, MOEQ_EPI_STORE);
+    const int64_t live = std::min<int64_t>(p.max_tiles, p.pairs + int64_t(m->n_shared)) *
+                         cdiv(m->hidden, bn);
+    const int64_t want = 1024;
+    int64_t s = cdiv(want, std::max<int64_t>(live, 1));
+    p.splits = int(std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(s, 8), m->inter / 128)));
+  }
+  p.y_dtype = p.splits > 1 ? MOEQ_F32 : MOEQ_F16;
+  const int Et = m->n_experts + m->n_shared;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = o;
+    o += align256(bytes);
+    return at;
+  };
+  p.off_idx = take(size_t(p.pairs) * 4);
+  p.off_w = take(size_t(p.pairs) * 4);
+  p.off_counts = take(size_t(Et) * 4);
+  p.off_offsets = take(size_t(Et + 1) * 4);
+  p.off_row_token = take(size_t(p.rows) * 4);
+  p.off_row_pair = take(size_t(p.pairs) * 4);
+  p.off_inv = take(size_t(p.pairs) * 4);
+  p.off_tiles = take(size_t(p.max_tiles) * 16);
+  p.off_ntiles = take(4);
+  p.off_perm = take(moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared));
+  p.off_h = take(size_t(p.rows) * m->inter * 2);
+  p.off_y = take(size_t(p.splits) * p.rows * m->hidden * (p.y_dtype == MOEQ_F32 ? 4 : 2));
+  p.total = o;
+  return p;
+}
+
+static int check_layer(const moeq_moe *m) {
+  if (!m) return fail(MOEQ_ERR_INVALID, "moe: null layer");
+  if (m->hidden <= 0 || m->inter <= 0 || m->n_experts <= 0 || m->top_k <= 0 || m->n_shared < 0)
+    return fail(MOEQ_ERR_INVALID, "moe: hidden=%d inter=%d n_experts=%d top_k=%d n_shared=%d", m->hidden,
+                m->inter, m->n_experts, m->top_k, m->n_shared);
+  if (m->top_k > m->n_experts) return fail(MOEQ_ERR_INVALID, "moe: top_k=%d > n_experts=%d", m->top_k, m->n_experts);
+  if (m->act_dtype != MOEQ_F16 && m->act_dtype != MOEQ_BF16) return fail(MOEQ_ERR_INVALID, "moe: act_dtype=%d", m->act_dtype);
+  if (m->gate_dtype != MOEQ_F16 && m->gate_dtype != MOEQ_BF16 && m->gate_dtype != MOEQ_F32)
+    return fail(MOEQ_ERR_INVALID, "moe: gate_dtype=%d", m->gate_dtype);
+  if (!m->gate_w) return fail(MOEQ_ERR_INVALID, "moe: gate_w is null");
+  if (m->w1.K != m->hidden || m->w1.N != m->inter || m->w3.K != m->hidden || m->w3.N != m->inter)
+    return fail(MOEQ_ERR_INVALID, "moe: gate/up projections must be [hidden=%d -> inter=%d]", m->hidden, m->inter);
+  if (m->w2.K != m->inter || m->w2.N != m->hidden)
+    return fail(MOEQ_ERR_INVALID, "moe: down projection must be [inter=%d -> hidden=%d]", m->inter, m->hidden);
+  return MOEQ_OK;
+}
+
+}  // namespace moeq
+
+using namespace moeq;
+
+extern "C" const char *moeq_last_error(void) { return g_err; }
+
+extern "C" int moeq_version(void) { return 1; }
+
+extern "C" size_t moeq_moe_workspace_size(const moeq_moe *m, int64_t T) {
+  if (check_layer(m) || T <= 0) return 0;
+  return make_plan(m, T).total;
+}
+
+extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out,
+                                int out_dtype, void *logits_out, void *ws, size_t ws_bytes,
+                                void *stream) {
+  int rc = check_layer(m);
+  if (rc) return rc;
+  if (!x || !out) return fail(MOEQ_ERR_INVALID, "moe: null x/out");
+  if (T <= 0) return fail(MOEQ_ERR_INVALID, "moe: T=%lld", (long long)T);
+  if (out_dtype != m->act_dtype && out_dtype != MOEQ_F32)
+    return fail(MOEQ_ERR_INVALID, "moe: out_dtype=%d must be act_dtype or F32", out_dtype);
+  const Plan p = make_plan(m, T);
+  if (!ws || ws_bytes < p.total)
+    return fail(MOEQ_ERR_WORKSPACE, "moe: workspace %zu < %zu bytes", ws_bytes, p.total);
+  char *base = static_cast<char *>(ws);
+  auto at = [&](size_t off) { return static_cast<void *>(base + off); };
+  int32_t *idx = static_cast<int32_t *>(at(p.off_idx));
+  float *w = static_cast<float *>(at(p.off_w));
+  int32_t *counts = static_cast<int32_t *>(at(p.off_counts));
+  int32_t *offsets = static_cast<int32_t *>(at(p.off_offsets));
+  int32_t *row_token = static_cast<int32_t *>(at(p.off_row_token));
+  int32_t *row_pair = static_cast<int32_t *>(at(p.off_row_pair));
+  int32_t *inv = static_cast<int32_t *>(at(p.off_inv));
+  int32_t *tiles = static_cast<int32_t *>(at(p.off_tiles));
+  int32_t *n_tiles = static_cast<int32_t *>(at(p.off_ntiles));
+
+  rc = moeq_route(x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
+                  m->top_k, m->norm_topk, logits_out, idx, w, stream);
+  if (rc) return rc;
+  rc = moeq_permute(idx, T, m->top_k, m->n_experts, m->n_shared, p.bm, counts, offsets, row_token,
+                    row_pair, inv, tiles, n_tiles, at(p.off_perm),
+                    moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared), stream);
+  if (rc) return rc;
+
+  moeq_gemm gu{};
+  gu.a = x;
+  gu.a_dtype = m->act_dtype;
+  gu.lda = m->hidden;
+  gu.row_src = row_token;
+  gu.tiles = tiles;
+  gu.n_tiles = n_tiles;
+  gu.max_tiles = p.max_tiles;
+  gu.bm = p.bm;
+  gu.epilogue = MOEQ_EPI_SILU_MUL;
+  gu.out = at(p.off_h);
+  gu.out_dtype = MOEQ_F16;
+  gu.ldo = m->inter;
+  gu.splits = 1;
+  gu.split_stride = 0;
+  rc = moeq_grouped_gemm(&gu, &m->w1, &m->w3, stream);
+  if (rc) return rc;
+
+  moeq_gemm dn = gu;
+  dn.a = at(p.off_h);
+  dn.a_dtype = MOEQ_F16;
+  dn.lda = m->inter;
+  dn.row_src = nullptr;
+  dn.epilogue = MOEQ_EPI_STORE;
+  dn.out = at(p.off_y);
+  dn.out_dtype = p.y_dtype;
+  dn.ldo = m->hidden;
+  dn.splits = p.splits;
+  dn.split_stride = p.rows * m->hidden;
+  rc = moeq_grouped_gemm(&dn, &m->w2, nullptr, stream);
+  if (rc) return rc;
+
+  return moeq_combine(at(p.off_y), p.y_dtype, p.splits, p.rows * m->hidden, m->hidden, inv, w, T,
+                      m->top_k, m->n_shared, m->hidden, out, out_dtype, stream);
+}
+
+// Launch plan introspection for tests and the benchmark (not a reference
+// interface): writes {bm, splits, max_tiles, y_dtype}.
+extern "C" int moeq_moe_plan(const moeq_moe *m, int64_t T, int32_t *out4) {
+  int rc = check_layer(m);
+  if (rc) return rc;
+  if (T <= 0 || !out4) return fail(MOEQ_ERR_INVALID, "moe_plan: T=%lld", (long long)T);
+  Plan p = make_plan(m, T);
+  out4[0] = p.bm;
+  out4[1] = p.splits;
+  out4[2] = p.max_tiles;
+  out4[3] = p.y_dtype;
+  return MOEQ_OK;
+}

@@ -1,0 +1,111 @@
+// Top-k weighted combine of the grouped expert outputs (plus shared experts).
+// One work-group per token, 8 columns per thread, fixed summation order
+// (slots ascending, split-K slices ascending), no atomics: bit-reproducible.
+#include <algorithm>
+
+#include "common.h"
+
+namespace moeq {
+
+template <int YDT>
+__device__ __forceinline__ void load_y8(const void *y, int64_t off, float (&v)[8]) {
+  if constexpr (YDT == MOEQ_F32) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(y) + off);
+    float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(y) + off);
+    uint32_t ws[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = f16_bits_to_f32(uint16_t(ws[j] & 0xffffu));
+      v[2 * j + 1] = f16_bits_to_f32(uint16_t(ws[j] >> 16));
+    }
+  }
+}
+
+template <int YDT>
+__global__ __launch_bounds__(256) void combine_kernel(
+    const void *y, int splits, int64_t split_stride, int64_t ldy, const int32_t *inv_perm,
+    const float *w, int64_t T, int k, int n_shared, int H, int64_t R, void *out, int out_dtype) {
+  for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
+    for (int c = 8 * threadIdx.x; c < H; c += 8 * blockDim.x) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < k; ++s) {
+        const int32_t r = inv_perm[t * k + s];
+        if (r < 0 || r >= R) continue;  // never for a schedule from moeq_permute
+        const float wt = w[t * k + s];
+        float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < splits; ++sp) {
+          float v[8];
+          load_y8<YDT>(y, sp * split_stride + int64_t(r) * ldy + c, v);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sum[j] += v[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wt, sum[j], acc[j]);
+      }
+      for (int v = 0; v < n_shared; ++v) {
+        const int64_t r = T * k + int64_t(v) * T + t;
+        for (int sp = 0; sp < splits; ++sp) {
+          float y8[8];
+          load_y8<YDT>(y, sp * split_stride + r * ldy + c, y8);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] += y8[j];
+        }
+      }
+      const int64_t o = t * H + c;
+      if (out_dtype == MOEQ_F32) {
+        float4 *p = reinterpret_cast<float4 *>(static_cast<float *>(out) + o);
+        p[0] = (float4){acc[0], acc[1], acc[2], acc[3]};
+        p[1] = (float4){acc[4], acc[5], acc[6], acc[7]};
+      } else {
+        uint32_t ws[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint16_t lo, hi;
+          if (out_dtype == MOEQ_BF16) {
+            lo = f32_to_bf16(acc[2 * j]);
+            hi = f32_to_bf16(acc[2 * j + 1]);
+          } else {
+            lo = f32_to_f16_bits(acc[2 * j]);
+            hi = f32_to_f16_bits(acc[2 * j + 1]);
+          }
+          ws[j] = uint32_t(lo) | (uint32_t(hi) << 16);
+        }
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o) = (uint4){ws[0], ws[1], ws[2], ws[3]};
+      }
+    }
+  }
+}
+
+}  // namespace moeq
+
+using namespace moeq;
+
+extern "C" int moeq_combine(const void *y, int y_dtype, int splits, int64_t split_stride,
+                            int64_t ldy, const int32_t *inv_perm, const float *w, int64_t T,
+                            int top_k, int n_shared, int H, void *out, int out_dtype,
+                            void *stream) {
+  if (!y || !inv_perm || !w || !out) return fail(MOEQ_ERR_INVALID, "combine: null pointer");
+  if (y_dtype != MOEQ_F16 && y_dtype != MOEQ_F32) return fail(MOEQ_ERR_INVALID, "combine: y_dtype=%d", y_dtype);
+  if (out_dtype != MOEQ_F16 && out_dtype != MOEQ_BF16 && out_dtype != MOEQ_F32)
+    return fail(MOEQ_ERR_INVALID, "combine: out_dtype=%d", out_dtype);
+  if (T <= 0 || top_k <= 0 || n_shared < 0 || splits < 1)
+    return fail(MOEQ_ERR_INVALID, "combine: T=%lld top_k=%d n_shared=%d splits=%d", (long long)T, top_k, n_shared, splits);
+  if (H <= 0 || H % 8 || ldy < H || ldy % 8)
+    return fail(MOEQ_ERR_INVALID, "combine: H=%d ldy=%lld (multiples of 8, ldy >= H)", H, (long long)ldy);
+  if (splits > 1 && split_stride < (T * top_k + int64_t(n_shared) * T) * ldy)
+    return fail(MOEQ_ERR_INVALID, "combine: split_stride=%lld too small", (long long)split_stride);
+  const int64_t R = T * top_k + int64_t(n_shared) * T;
+  dim3 grid(unsigned(std::min<int64_t>(T, 65535))), block(256);
+  hipStream_t s = as_stream(stream);
+  if (y_dtype == MOEQ_F32)
+    combine_kernel<MOEQ_F32><<<grid, block, 0, s>>>(y, splits, split_stride, ldy, inv_perm, w, T,
+                                                   top_k, n_shared, H, R, out, out_dtype);
+  else
+    combine_kernel<MOEQ_F16><<<grid, block, 0, s>>>(y, splits, split_stride, ldy, inv_perm, w, T,
+                                                   top_k, n_shared, H, R, out, out_dtype);
+  return check_launch("combine");
+}

@@ -1,0 +1,239 @@
+"""GPU parity of each stage of the HIP path against the CPU oracle.
+
+Integer / index outputs (packed words, routing indices, the permutation, tile
+schedule) must match bit for bit; router logits too (same pinned fp32 order);
+fp results (routing weights, GEMMs) within stated tolerances.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import relative_error, to_np
+from oracle import quant as oq
+from oracle import route as orr
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# ----------------------------------------------------------------- layouts
+@pytest.mark.parametrize("nbits", [1, 2, 3, 4])
+def test_pack_and_repack_bit_exact(device, nbits):
+    from robustgemq_amd import ops
+    from robustgemq_amd.experts import QuantProjection
+    _say(f"[pack/repack] nbits={nbits}")
+    rng = np.random.default_rng(nbits)
+    N, K = 96, 640  # K not a multiple of eps for 3-bit: exercises the tail
+    codes = rng.integers(0, 1 << nbits, size=(N, K)).astype(np.uint8)
+    words, eps = ops.pack_weights_over_cols(torch.from_numpy(codes).to(device), nbits)
+    assert eps == 32 // nbits
+    np.testing.assert_array_equal(to_np(words).view(np.uint32), oq.pack_cols(codes, nbits).view(np.uint32))
+    back = ops.unpack_words(words, nbits, K)
+    np.testing.assert_array_equal(to_np(back), codes)
+    # build layout through QuantProjection (moeq_repack + moeq_prep_scales)
+    G = K // 64
+    s = (rng.standard_normal((G, N)) * 0.01).astype(np.float16)
+    z = rng.integers(0, 1 << nbits, size=(G, N)).astype(np.float16)
+    Kb = 512
+    codes_b = codes[:, :Kb]
+    wb, _ = ops.pack_weights_over_cols(torch.from_numpy(codes_b).to(device), nbits)
+    proj = QuantProjection([wb], [torch.from_numpy(s[:Kb // 64]).to(device)], [torch.from_numpy(z[:Kb // 64]).to(device)],
+                           [nbits], Kb, N, 64, 0)
+    np.testing.assert_array_equal(to_np(proj.words).view(np.uint32).reshape(Kb // 128, N, 4, nbits),
+                                  oq.repack_build(codes_b, nbits))
+    np.testing.assert_array_equal(to_np(proj.sz).view(np.uint32), oq.prep_scales(s[:Kb // 64], z[:Kb // 64], 0))
+
+
+# ------------------------------------------------------------------ routing
+@pytest.mark.parametrize("gate", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("T,H,E,k,norm", [(1, 2048, 64, 8, False), (333, 2048, 64, 8, False),
+                                         (257, 2048, 128, 8, True), (64, 4096, 8, 2, True),
+                                         (40, 1536, 64, 6, False), (16, 512, 8, 2, False)])
+def test_route_bit_exact(device, gate, T, H, E, k, norm):
+    from robustgemq_amd import ops
+    _say(f"[route] gate={gate} T={T} H={H} E={E} k={k}")
+    g = torch.Generator().manual_seed(T + H + E)
+    act = torch.bfloat16 if gate == "bf16" else torch.float16
+    x = torch.randn(T, H, generator=g).to(act)
+    wg = (torch.randn(E, H, generator=g) * 0.02).to(act)
+    gw = wg.float() if gate == "f32" else wg
+    lg, idx, w = ops.route(x.to(device), gw.to(device), k, norm)
+    x32 = x.float().numpy()
+    ref_lg = orr.router_logits(x32, wg.float().numpy(), gate)
+    np.testing.assert_array_equal(lg.float().cpu().numpy().view(np.uint32), ref_lg.view(np.uint32))
+    ref_idx, ref_w = orr.topk_route(ref_lg, k, norm)
+    np.testing.assert_array_equal(to_np(idx), ref_idx)
+    np.testing.assert_allclose(to_np(w), ref_w, rtol=2e-6, atol=1e-7)
+    # same selection from the logits alone
+    idx2, w2 = ops.route_from_logits(lg, k, norm)
+    np.testing.assert_array_equal(to_np(idx2), ref_idx)
+    np.testing.assert_allclose(to_np(w2), ref_w, rtol=2e-6, atol=1e-7)
+
+
+def test_route_bias_and_ties(device):
+    from robustgemq_amd import ops
+    _say("[route] bias + ties")
+    T, H, E, k = 50, 512, 16, 4
+    x = torch.zeros(T, H, dtype=torch.float16)
+    wg = torch.zeros(E, H, dtype=torch.float16)
+    bias = torch.tensor([0.5 if e % 3 == 0 else 0.0 for e in range(E)], dtype=torch.float32)
+    lg, idx, w = ops.route(x.to(device), wg.float().to(device), k, True, logit_bias=bias.to(device))
+    # all-zero logits plus bias: experts 0, 3, 6, 9 tie at 0.5 and win in index order
+    assert (to_np(idx) == np.array([0, 3, 6, 9])).all()
+    np.testing.assert_allclose(to_np(w), 0.25, rtol=1e-6)
+
+
+@pytest.mark.parametrize("T,k,E,S,bm", [(1, 8, 64, 0, 16), (1, 6, 64, 2, 16), (700, 2, 8, 0, 64),
+                                        (2048, 8, 64, 0, 128), (4096, 8, 128, 0, 128),
+                                        (300, 6, 64, 2, 32), (5000, 1, 3, 0, 128)])
+def test_permute_bit_exact(device, T, k, E, S, bm):
+    from robustgemq_amd import ops
+    _say(f"[permute] T={T} k={k} E={E} shared={S} bm={bm}")
+    rng = np.random.default_rng(T * 7 + E)
+    p = np.exp(-2.0 * rng.random(E))
+    p /= p.sum()
+    idx = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    out = ops.permute(torch.from_numpy(idx).to(device), E, n_shared=S, bm=bm)
+    ref = orr.permute(idx, E, n_shared=S)
+    for key in ("counts", "offsets", "row_token", "row_pair", "inv_perm"):
+        np.testing.assert_array_equal(to_np(out[key]), ref[key], err_msg=key)
+    # tile schedule: covers each expert's rows exactly once, <= bm rows, in order
+    nt = int(to_np(out["n_tiles"])[0])
+    assert 0 < nt <= out["max_tiles"]
+    tiles = to_np(out["tiles"])[:nt]
+    covered = np.zeros(T * k + S * T, np.int32)
+    for e, r0, rc, _ in tiles:
+        assert 0 < rc <= bm
+        assert ref["offsets"][e] <= r0 and r0 + rc <= ref["offsets"][e + 1]
+        covered[r0:r0 + rc] += 1
+    assert (covered == 1).all()
+
+
+# ------------------------------------------------------------- grouped GEMM
+def _make_proj(device, rng, E, K, N, bits, g, mode):
+    from robustgemq_amd.experts import QuantProjection, pack_codes
+    codes, s_l, z_l, words = [], [], [], []
+    for e in range(E):
+        b = bits[e]
+        c = rng.integers(0, 1 << b, size=(N, K)).astype(np.uint8)
+        s = (np.abs(rng.standard_normal((K // g, N))) * 0.01 + 1e-3).astype(np.float16)
+        if mode == 0:
+            z = rng.integers(0, 1 << b, size=(K // g, N)).astype(np.float16)
+            if b == 1:
+                z[:] = 0.5
+        else:
+            z = (rng.standard_normal((K // g, N)) * 0.02).astype(np.float16)
+        codes.append(c)
+        s_l.append(s)
+        z_l.append(z)
+        words.append(pack_codes(torch.from_numpy(c).to(device), b))
+    proj = QuantProjection(words, [torch.from_numpy(s).to(device) for s in s_l],
+                           [torch.from_numpy(z).to(device) for z in z_l], bits, K, N, g, mode)
+    dense = []
+    for c, s, z in zip(codes, s_l, z_l):
+        if mode == 0:
+            W = oq.kernel_dequant_hqq(c, s, z, g)  # [K, N] fp16, == fake-quant weight
+        else:
+            gi = np.arange(K) // g
+            W = oq.dequant_affine(c.T.astype(np.float16), s[gi, :], z[gi, :])
+        dense.append(W.astype(np.float32))
+    return proj, dense
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("g", [64, 128])
+def test_grouped_gemm_store_matches_fp32(device, bm, mode, g):
+    from robustgemq_amd import ops
+    _say(f"[gemm/store] bm={bm} mode={mode} g={g}")
+    rng = np.random.default_rng(bm + 10 * mode + g)
+    E, K, N = 5, 384, 160  # N not a multiple of the column tile
+    bits = [1, 2, 3, 4, 2]
+    proj, dense = _make_proj(device, rng, E, K, N, bits, g, mode)
+    counts = [bm * 2 + 3, 1, 0, 17, bm - 5]
+    rows = sum(counts)
+    T = 61
+    x = (rng.standard_normal((T, K)) * 0.5).astype(np.float16)
+    row_src = rng.integers(0, T, size=rows).astype(np.int32)
+    tiles, r = [], 0
+    for e, m in enumerate(counts):
+        for j in range(0, m, bm):
+            tiles.append((e, r + j, min(bm, m - j), 0))
+        r += m
+    tt = torch.tensor(tiles, dtype=torch.int32, device=device)
+    n = torch.tensor([len(tiles)], dtype=torch.int32, device=device)
+    out = ops.grouped_gemm(torch.from_numpy(x).to(device), rows, N, tt, n, len(tiles) + 3, bm, proj,
+                           row_src=torch.from_numpy(row_src).to(device), out_dtype=torch.float32)
+    ref = np.zeros((rows, N), np.float32)
+    r = 0
+    for e, m in enumerate(counts):
+        ref[r:r + m] = x[row_src[r:r + m]].astype(np.float32) @ dense[e]
+        r += m
+    got = to_np(out)
+    assert relative_error(got, ref) < 2e-6
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("bm", [16, 128])
+@pytest.mark.parametrize("adt", [torch.float16, torch.bfloat16])
+def test_grouped_gemm_silu_mul_and_splitk(device, bm, adt):
+    from robustgemq_amd import ops
+    _say(f"[gemm/silu+splitk] bm={bm} act={adt}")
+    rng = np.random.default_rng(bm)
+    E, K, N = 3, 512, 256
+    bits = [2, 3, 4]
+    p1, d1 = _make_proj(device, rng, E, K, N, bits, 64, 0)
+    p3, d3 = _make_proj(device, rng, E, K, N, bits, 64, 0)
+    counts = [40, 7, 130]
+    rows = sum(counts)
+    x = torch.from_numpy((rng.standard_normal((rows, K)) * 0.5).astype(np.float32)).to(adt)
+    tiles, r = [], 0
+    for e, m in enumerate(counts):
+        for j in range(0, m, bm):
+            tiles.append((e, r + j, min(bm, m - j), 0))
+        r += m
+    tt = torch.tensor(tiles, dtype=torch.int32, device=device)
+    n = torch.tensor([len(tiles)], dtype=torch.int32, device=device)
+    h = ops.grouped_gemm(x.to(device), rows, N, tt, n, len(tiles), bm, p1, p1=p3)
+    x32 = x.float().numpy()
+    ref = np.zeros((rows, N), np.float32)
+    r = 0
+    for e, m in enumerate(counts):
+        g_ = x32[r:r + m] @ d1[e]
+        u = x32[r:r + m] @ d3[e]
+        ref[r:r + m] = g_ / (1 + np.exp(-g_)) * u
+        r += m
+    assert relative_error(to_np(h).astype(np.float32), ref) < 1e-3
+    # split-K store of the same first projection
+    y = ops.grouped_gemm(x.to(device), rows, N, tt, n, len(tiles), bm, p1, out_dtype=torch.float32, splits=3)
+    assert tuple(y.shape) == (3, rows, N)
+    ys = to_np(y).sum(axis=0)
+    r = 0
+    for e, m in enumerate(counts):
+        np.testing.assert_allclose(ys[r:r + m], x32[r:r + m] @ d1[e], rtol=1e-4, atol=1e-4)
+        r += m
+
+
+def test_combine_deterministic_order(device):
+    from robustgemq_amd import ops
+    _say("[combine]")
+    rng = np.random.default_rng(0)
+    T, k, S, H = 37, 3, 2, 256
+    rows = T * k + S * T
+    y = rng.standard_normal((2, rows, H)).astype(np.float32)
+    perm = rng.permutation(T * k).astype(np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    out = ops.combine(torch.from_numpy(y).to(device), torch.from_numpy(perm).to(device),
+                      torch.from_numpy(w).to(device), T, k, S, torch.float32)
+    ys = y.sum(axis=0)
+    ref = np.zeros((T, H), np.float32)
+    for t in range(T):
+        for s in range(k):
+            ref[t] += w[t, s] * ys[perm[t * k + s]]
+        for v in range(S):
+            ref[t] += ys[T * k + v * T + t]
+    np.testing.assert_allclose(to_np(out), ref, rtol=1e-5, atol=1e-5)
