@@ -1,0 +1,263 @@
+"""MoE-layer benchmark on one MI355X (BASELINE.json metric).
+
+Workload (configs[1] of BASELINE.json): OLMoE-1B-7B-shaped layer, hidden 2048,
+64 experts of intermediate 1024, top-8 softmax routing, per-expert 2/3/4-bit
+(50/25/25) group-64 HQQ weights, fp16 activations, synthetic data.  A step is
+one full layer forward (route, permute, grouped gate/up + SiLU*mul, grouped
+down, combine) over a 2048-token prefill batch already resident in HBM;
+`value` is prefill tokens/s.  The same run also reports prefill at 512 tokens
+and decode at batch 1 / 8 / 32 (graph-replayed, as the reference times decode
+under CUDA graphs), the live roofline of the dominant kernel (the grouped
+gate/up GEMM, MFMA-bound at this size), and the CPU baseline: the oracle's
+fp32 dequantize-then-matmul expert loop on a bounded token sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+                       [--tokens T] [--no-cpu] [--no-decode]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer prefill+decode tokens/sec on 1 GPU; % HBM BW / % MFMA peak"
+PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="olmoe_mixed")
+    ap.add_argument("--tokens", type=int, default=2048)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_events(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps  # ms
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
+                                   "(the expert path is single-GPU here, multi-GPU sharding is design-only)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from robustgemq_amd import ops
+    from robustgemq_amd.synthetic import CONFIGS, build_block, flops, make_inputs, make_weights
+
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    T = args.tokens
+    log(f"[bench] building {cfg.name} (synthetic weights, seed 0)")
+    w = make_weights(cfg, seed=0, quant_device=dev)
+    block = build_block(cfg, w, device=dev)
+    layer = block._layer
+    x = make_inputs(cfg, T, seed=0).to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    # ---------------- the timed step: full layer forward, T tokens
+    out = torch.empty((T, cfg.hidden), dtype=cfg.act_dtype, device=dev)
+    logits = torch.empty((T, cfg.n_experts), dtype=torch.float32 if cfg.family == "deepseekv2" else cfg.act_dtype,
+                         device=dev)
+
+    def step():
+        layer.forward(x, out=out, logits=logits)
+
+    log(f"[bench] prefill T={T}: warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    value = T * args.steps / wall
+
+    # ---------------- stage timings and the dominant kernel's live roofline
+    _, idx, wt = ops.route(x, layer.gate_w, layer.top_k, layer.norm_topk, logits=False, logit_bias=layer.logit_bias)
+    plan = layer.plan(T)
+    bm = plan["bm"]
+    perm = ops.permute(idx, layer.n_experts, layer.n_shared, bm=bm)
+    rows = T * layer.top_k + layer.n_shared * T
+    counts = perm["counts"].cpu().numpy()
+    hit = [e for e in range(layer.n_experts + layer.n_shared) if counts[e] > 0]
+
+    def gate_up():
+        return ops.grouped_gemm(x, rows, layer.inter, perm["tiles"], perm["n_tiles"], perm["max_tiles"], bm,
+                                layer.w1, p1=layer.w3, row_src=perm["row_token"])
+
+    h = gate_up()
+
+    def down():
+        return ops.grouped_gemm(h, rows, layer.hidden, perm["tiles"], perm["n_tiles"], perm["max_tiles"], bm,
+                                layer.w2, out_dtype=torch.float16)
+
+    def route_only():
+        ops.route(x, layer.gate_w, layer.top_k, layer.norm_topk, logits=True, logit_bias=layer.logit_bias)
+
+    def permute_only():
+        ops.permute(idx, layer.n_experts, layer.n_shared, bm=bm)
+
+    y = down()
+
+    def combine_only():
+        ops.combine(y, perm["inv_perm"], wt, T, layer.top_k, layer.n_shared, cfg.act_dtype)
+
+    kt = {}
+    for name, fn in (("route", route_only), ("permute", permute_only), ("gate_up", gate_up), ("down", down),
+                     ("combine", combine_only)):
+        kt[name] = time_events(fn, args.steps, 3, stream)
+    gu_flops = 2.0 * rows * 2 * cfg.hidden * cfg.inter
+    dn_flops = 2.0 * rows * cfg.hidden * cfg.inter
+    gu_tflops = gu_flops / (kt["gate_up"] * 1e-3) / 1e12
+    w_bytes_gu = layer.w1.weight_bytes(hit) + layer.w3.weight_bytes(hit)
+    roofline = {"bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(gu_tflops / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
+                "kernel": "grouped_gemm_kernel<BM=%d> gate/up (SiLU*mul epilogue)" % bm,
+                "flops_per_launch": gu_flops, "avg_launch_ms": round(kt["gate_up"], 4)}
+    layer_flops = flops(cfg, T)
+    extra = {
+        "stage_ms": {k: round(v, 4) for k, v in kt.items()},
+        "layer_tflops": round(layer_flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "down_tflops": round(dn_flops / (kt["down"] * 1e-3) / 1e12, 2),
+        "gate_up_weight_bytes": w_bytes_gu, "plan": plan, "hit_experts": len(hit),
+    }
+
+    # ---------------- secondary lines: prefill 512, decode (graph replay)
+    runs = {}
+    for tp in [t for t in cfg.runs.get("prefill", ()) if t != T]:
+        xp = make_inputs(cfg, tp, seed=1).to(dev)
+        ms = time_events(lambda: layer.forward(xp, want_logits=False), args.steps, args.warmup, stream)
+        runs[f"prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4)}
+    if not args.no_decode:
+        for B in cfg.runs.get("decode", ()):
+            xb = make_inputs(cfg, B, seed=2).to(dev)
+            ob = torch.empty((B, cfg.hidden), dtype=cfg.act_dtype, device=dev)
+            layer.forward(xb, out=ob, want_logits=False)  # sizes the workspace before capture
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream(dev)
+            s.wait_stream(stream)
+            with torch.cuda.stream(s):
+                layer.forward(xb, out=ob, want_logits=False)
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    layer.forward(xb, out=ob, want_logits=False)
+            stream.wait_stream(s)
+            ref = ob.clone()
+            ms_graph = time_events(g.replay, args.steps * 5, args.warmup, stream)
+            assert torch.equal(ob, ref), "graph replay changed the decode output"
+            ms_eager = time_events(lambda: layer.forward(xb, out=ob, want_logits=False), args.steps, args.warmup,
+                                   stream)
+            idx_b = ops.route(xb, layer.gate_w, layer.top_k, layer.norm_topk, logits=False)[1]
+            hit_b = sorted(set(idx_b.cpu().numpy().reshape(-1).tolist()))
+            bytes_b = (layer.w1.weight_bytes(hit_b) + layer.w3.weight_bytes(hit_b) + layer.w2.weight_bytes(hit_b)
+                       + cfg.n_experts * cfg.hidden * 2 + 2 * B * cfg.hidden * 2)
+            runs[f"decode_B{B}"] = {"tokens_per_s": round(B / (ms_graph * 1e-3), 1), "ms_graph": round(ms_graph, 4),
+                                    "ms_eager": round(ms_eager, 4), "hit_experts": len(hit_b),
+                                    "alg_bytes": bytes_b,
+                                    "hbm_frac_layer": round(bytes_b / (ms_graph * 1e-3) / (PEAK_HBM_GBS * 1e9), 4)}
+    extra["runs"] = runs
+
+    # ---------------- CPU baseline: oracle fp32 expert loop, bounded sample
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, w, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name} MoE layer, prefill T={T} (BASELINE configs[1])", "hidden": cfg.hidden,
+                   "inter": cfg.inter, "experts": cfg.n_experts, "top_k": cfg.top_k, "group_size": cfg.group_size,
+                   "bits": dict(sorted({b: w["bits"].count(b) for b in set(w["bits"])}.items())),
+                   "tokens": T, "act_dtype": str(cfg.act_dtype).replace("torch.", "")},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(cfg, w, budget_s):
+    """Oracle fp32 dequantize-then-matmul loop (the reference's forward_n_tokens
+    restated, gemq/inference/moe_block.py:781-815) on a bounded token sample;
+    dense weights are materialized before timing, as the reference's fake
+    model holds them."""
+    import numpy as np
+    import threadpoolctl
+    import torch
+
+    from oracle import moe as om
+    from oracle import quant as oq
+    from robustgemq_amd.synthetic import make_inputs
+
+    log("[bench] cpu baseline: dequantizing weights on the host")
+
+    def dense(t):
+        N, K = t.shape
+        return oq.dequant_hqq(t.Q.cpu().numpy(), t.scales.cpu().numpy(), t.zeros.cpu().numpy()).reshape(
+            N, K).astype(np.float32)
+
+    W1 = [dense(e["gate_proj"]) for e in w["experts"]]
+    W3 = [dense(e["up_proj"]) for e in w["experts"]]
+    W2 = [dense(e["down_proj"]) for e in w["experts"]]
+    gate = w["gate"].float().numpy()
+    ldt = "f16" if cfg.act_dtype == torch.float16 else "bf16"
+    Ts = 256
+    x = make_inputs(cfg, Ts, seed=3).float().numpy()
+    cores = os.cpu_count()
+    with threadpoolctl.threadpool_limits(limits=cores):
+        info = threadpoolctl.threadpool_info()
+        threads = max([i.get("num_threads", 1) for i in info] or [1])
+        om.moe_forward(x, gate, ldt, cfg.top_k, cfg.norm_topk, W1, W3, W2)  # warm-up
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+            t0 = time.perf_counter()
+            om.moe_forward(x, gate, ldt, cfg.top_k, cfg.norm_topk, W1, W3, W2)
+            times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(Ts / med, 1), "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": f"{Ts}-token prefill of the same layer (median of {len(times)} reps, "
+                      f"fp32 numpy BLAS, weights pre-dequantized), host {model} x{cores}"}
+
+
+if __name__ == "__main__":
+    main()
