@@ -107,15 +107,18 @@ int moeq_prep_scales(const uint16_t *scales, const uint16_t *zeros,
  * the reference has none), rounded to x_dtype unless gate_dtype is
  * MOEQ_F32; then p = softmax_fp32(logits),
  * top_k experts ranked by logit (ties: lower index first), optional
- * renormalisation.  logits_out may be NULL.
+ * renormalisation.  logits_out may be NULL; the rounded logits are then kept
+ * in ws (moeq_route_workspace_size bytes), which is unused otherwise.
  * Replaces the router of QuantFused*MoEBlock.forward_n_tokens /
  * forward_one_token: gemq/inference/moe_block.py:790-797 (OLMoE), :243-249
  * (Mixtral, always renormalized), :1020-1027 (Qwen3), :549-556 (DeepSeek,
  * fp32 gate), :828-833 (decode). */
+size_t moeq_route_workspace_size(int64_t T, int E);
 int moeq_route(const void *x, int x_dtype, int64_t T, int H,
                const void *gate_w, int gate_dtype, const float *logit_bias,
                int E, int top_k, int norm_topk, void *logits_out,
-               int32_t *idx_out, float *w_out, void *stream);
+               int32_t *idx_out, float *w_out, void *ws, size_t ws_bytes,
+               void *stream);
 
 /* Same selection and weights from given logits [T, E] (dtype F16/BF16/F32).
  * Used for externally biased routing (e.g. a Zipf popularity prior). */
@@ -130,8 +133,9 @@ int moeq_route_from_logits(const void *logits, int dtype, int64_t T, int E,
  *   row_token[T*top_k + n_shared*T]  token feeding each grouped row,
  *   row_pair[T*top_k]                t*top_k + slot of each routed row,
  *   inv_perm[T*top_k]                row of each (t, slot) pair,
- *   tiles[max_tiles*4]               (expert, row_start, row_count, 0) row
- *                                    tiles of at most `bm` rows,
+ *   tiles[max_tiles*4]               (expert, row_start, row_count, 0): each
+ *                                    expert's rows as full `bm`-row tiles
+ *                                    plus one remainder tile,
  *   n_tiles[1].
  * max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm).
  * Replaces the one_hot / nonzero / torch.where grouping and its host syncs,
@@ -151,7 +155,7 @@ int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
 
 typedef struct moeq_gemm {
   const void *a;            /* activations, rows addressed via row_src      */
-  int32_t a_dtype;          /* MOEQ_F16 | MOEQ_BF16                          */
+  int32_t a_dtype;          /* MOEQ_F16 (any bm) | MOEQ_BF16 (bm == 16)      */
   int64_t lda;              /* elements                                      */
   const int32_t *row_src;   /* [rows] source row of each grouped row, NULL = identity */
   const int32_t *tiles;     /* from moeq_permute (or built by the caller)    */

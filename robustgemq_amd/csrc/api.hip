@@ -32,7 +32,7 @@ struct Plan {
   int bm, splits, max_tiles, y_dtype;
   int64_t T, pairs, rows;
   size_t off_idx, off_w, off_counts, off_offsets, off_row_token, off_row_pair, off_inv,
-      off_tiles, off_ntiles, off_perm, off_h, off_y, total;
+      off_tiles, off_ntiles, off_perm, off_route, off_x16, off_h, off_y, total;
 };
 
 static Plan make_plan(const moeq_moe *m, int64_t T) {
@@ -71,10 +71,26 @@ static Plan make_plan(const moeq_moe *m, int64_t T) {
   p.off_tiles = take(size_t(p.max_tiles) * 16);
   p.off_ntiles = take(4);
   p.off_perm = take(moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared));
+  p.off_route = take(moeq_route_workspace_size(T, m->n_experts));
+  // the LDS-staged GEMM tiles (bm >= 32) read F16 rows
+  p.off_x16 = take(m->act_dtype == MOEQ_BF16 && p.bm >= 32 ? size_t(T) * m->hidden * 2 : 0);
   p.off_h = take(size_t(p.rows) * m->inter * 2);
   p.off_y = take(size_t(p.splits) * p.rows * m->hidden * (p.y_dtype == MOEQ_F32 ? 4 : 2));
   p.total = o;
   return p;
+}
+
+__global__ void bf16_to_f16_kernel(const uint16_t *x, int64_t n, uint16_t *y) {
+  const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;  // n is a multiple of 8
+  const uint4 u = *reinterpret_cast<const uint4 *>(x + i);
+  const uint32_t ws[4] = {u.x, u.y, u.z, u.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = uint32_t(f32_to_f16_bits(__uint_as_float(ws[j] << 16))) |
+           (uint32_t(f32_to_f16_bits(__uint_as_float(ws[j] & 0xffff0000u))) << 16);
+  *reinterpret_cast<uint4 *>(y + i) = (uint4){o[0], o[1], o[2], o[3]};
 }
 
 static int check_layer(const moeq_moe *m) {
@@ -132,16 +148,28 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
   int32_t *n_tiles = static_cast<int32_t *>(at(p.off_ntiles));
 
   rc = moeq_route(x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
-                  m->top_k, m->norm_topk, logits_out, idx, w, stream);
+                  m->top_k, m->norm_topk, logits_out, idx, w, at(p.off_route),
+                  moeq_route_workspace_size(T, m->n_experts), stream);
   if (rc) return rc;
   rc = moeq_permute(idx, T, m->top_k, m->n_experts, m->n_shared, p.bm, counts, offsets, row_token,
                     row_pair, inv, tiles, n_tiles, at(p.off_perm),
                     moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared), stream);
   if (rc) return rc;
 
+  const void *xa = x;
+  int xa_dtype = m->act_dtype;
+  if (m->act_dtype == MOEQ_BF16 && p.bm >= 32) {
+    const int64_t n = T * m->hidden;
+    bf16_to_f16_kernel<<<dim3(unsigned(cdiv(n / 8, 256))), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<const uint16_t *>(x), n, static_cast<uint16_t *>(at(p.off_x16)));
+    if ((rc = check_launch("moe/bf16_to_f16"))) return rc;
+    xa = at(p.off_x16);
+    xa_dtype = MOEQ_F16;
+  }
+
   moeq_gemm gu{};
-  gu.a = x;
-  gu.a_dtype = m->act_dtype;
+  gu.a = xa;
+  gu.a_dtype = xa_dtype;
   gu.lda = m->hidden;
   gu.row_src = row_token;
   gu.tiles = tiles;

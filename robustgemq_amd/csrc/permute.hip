@@ -54,79 +54,106 @@ __global__ __launch_bounds__(256) void hist_kernel(const int32_t *idx, int64_t T
     for (int e = lane; e < E; e += 64) cc[chunk * E + e] = cnt[e];
 }
 
-// Single block.  cc[nchunks][E] (chunk counts) becomes the first row of each
-// (chunk, expert) in place.
+// Exclusive prefix sum of one int per thread over the whole block (blockDim
+// a multiple of 64, <= 1024).  `sh` holds >= 17 ints of LDS; *total gets the
+// block sum.  Contains barriers: every thread of the block must call it.
+__device__ int block_exclusive_scan(int v, int *sh, int *total) {
+  const int lane = lane_id(), w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) sh[w] = incl;
+  __syncthreads();
+  if (w == 0) {
+    int tv = lane < nw ? sh[lane] : 0, ti = tv;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      int t = __shfl_up(ti, o);
+      if (lane >= o) ti += t;
+    }
+    if (lane < nw) sh[lane] = ti - tv;
+    if (lane == nw - 1) sh[16] = ti;
+  }
+  __syncthreads();
+  const int r = sh[w] + incl - v;
+  *total = sh[16];
+  __syncthreads();
+  return r;
+}
+
+// Row tiles of an expert with m rows: full bm-row tiles and one remainder
+// tile (the GEMM rounds a tile's active rows up to 2, 4 or 8 blocks of 16);
+// returns the count, *rt the tile height.
+__device__ __forceinline__ int tiles_of(int m, int bm, int *rt) {
+  *rt = bm;
+  return m <= 0 ? 0 : (m + bm - 1) / bm;
+}
+
+// Given per-expert row counts (one per thread e < Et), writes counts,
+// offsets, the tile schedule and the shared-expert rows; returns this
+// expert's first row.  Every thread of the block must call it.
+__device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_tiles,
+                        int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *tiles,
+                        int32_t *n_tiles, int *sh, int *s_off) {
+  const int e = threadIdx.x, Et = E + n_shared;
+  int rt;
+  const int nt = e < Et ? tiles_of(c, bm, &rt) : 0;
+  int tot_rows, tot_tiles;
+  const int off = block_exclusive_scan(e < Et ? c : 0, sh, &tot_rows);
+  const int tb = block_exclusive_scan(nt, sh, &tot_tiles);
+  if (e < Et) {
+    counts[e] = c;
+    offsets[e] = off;
+    s_off[e] = off;
+  }
+  if (e == 0) {
+    offsets[Et] = tot_rows;
+    // moeq_max_tiles bounds the count for any routing; the clamp only keeps
+    // a corrupted idx from writing past the schedule buffer
+    *n_tiles = min(tot_tiles, max_tiles);
+  }
+  for (int j = 0; j < nt && tb + j < max_tiles; ++j) {
+    const int r0 = j * rt;
+    int32_t *tp = tiles + 4 * (tb + j);
+    tp[0] = e;
+    tp[1] = off + r0;
+    tp[2] = min(rt, c - r0);
+    tp[3] = 0;
+  }
+  __syncthreads();
+  for (int v = 0; v < n_shared; ++v)
+    for (int64_t t = threadIdx.x; t < T; t += blockDim.x) row_token[s_off[E + v] + t] = int32_t(t);
+  return off;
+}
+
+// Single block of 1024 threads.  cc[nchunks][E] (chunk counts) becomes the
+// first row of each (chunk, expert) in place.
 __global__ __launch_bounds__(1024) void scan_kernel(
     int32_t *cc, int64_t nchunks, int64_t T, int k, int E, int n_shared, int bm,
     int max_tiles, int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *tiles,
     int32_t *n_tiles) {
-  __shared__ int32_t s_cnt[kMaxExperts];
-  __shared__ int32_t s_off[kMaxExperts + 1];
-  __shared__ int32_t s_ntile[kMaxExperts];
-  __shared__ int32_t s_rt[kMaxExperts];
-  __shared__ int32_t s_tbase[kMaxExperts + 1];
-  const int Et = E + n_shared;
-  for (int e = threadIdx.x; e < Et; e += blockDim.x) {
-    int32_t c = 0;
-    if (e < E)
-      for (int64_t ch = 0; ch < nchunks; ++ch) c += cc[ch * E + e];
-    else
-      c = int32_t(T);
-    s_cnt[e] = c;
-    counts[e] = c;
+  __shared__ int sh[17];
+  __shared__ int s_off[kMaxExperts];
+  const int e = threadIdx.x;
+  int c = 0;
+  if (e < E) {
+#pragma unroll 8
+    for (int64_t ch = 0; ch < nchunks; ++ch) c += cc[ch * E + e];
+  } else if (e < E + n_shared) {
+    c = int(T);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t run = 0, trun = 0;
-    for (int e = 0; e < Et; ++e) {
-      s_off[e] = run;
-      run += s_cnt[e];
-      // ceil(m / bm) tiles of near-equal height, rounded up to 16 rows
-      int32_t m = s_cnt[e], nt = 0, rt = 16;
-      if (m > 0) {
-        int32_t nmt = (m + bm - 1) / bm;
-        rt = ((m + nmt - 1) / nmt + 15) / 16 * 16;
-        nt = (m + rt - 1) / rt;
-      }
-      s_ntile[e] = nt;
-      s_rt[e] = rt;
-      s_tbase[e] = trun;
-      trun += nt;
+  const int off = schedule(c, E, n_shared, T, bm, max_tiles, counts, offsets, row_token, tiles, n_tiles, sh,
+                           s_off);
+  if (e < E) {
+    int run = off;
+    for (int64_t ch = 0; ch < nchunks; ++ch) {
+      const int v = cc[ch * E + e];
+      cc[ch * E + e] = run;
+      run += v;
     }
-    s_off[Et] = run;
-    s_tbase[Et] = trun;
-    // moeq_max_tiles bounds trun for any routing; the clamp only keeps a
-    // corrupted idx from writing past the schedule buffer
-    *n_tiles = min(trun, max_tiles);
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e <= Et; e += blockDim.x) offsets[e] = s_off[e];
-  for (int e = threadIdx.x; e < Et; e += blockDim.x) {
-    int32_t m = s_cnt[e], nt = s_ntile[e], rt = s_rt[e];
-    if (nt > 0) {
-      for (int32_t j = 0; j < nt && s_tbase[e] + j < max_tiles; ++j) {
-        int32_t r0 = j * rt;
-        int32_t rc = min(rt, m - r0);
-        int32_t *tp = tiles + 4 * (s_tbase[e] + j);
-        tp[0] = e;
-        tp[1] = s_off[e] + r0;
-        tp[2] = rc;
-        tp[3] = 0;
-      }
-    }
-    if (e < E) {
-      int32_t run = s_off[e];
-      for (int64_t ch = 0; ch < nchunks; ++ch) {
-        int32_t c = cc[ch * E + e];
-        cc[ch * E + e] = run;
-        run += c;
-      }
-    }
-  }
-  // shared experts: T rows each, token order
-  for (int v = 0; v < n_shared; ++v) {
-    int32_t base = s_off[E + v];
-    for (int64_t t = threadIdx.x; t < T; t += blockDim.x) row_token[base + t] = int32_t(t);
   }
 }
 
@@ -178,6 +205,99 @@ __global__ __launch_bounds__(256) void scatter_kernel(const int32_t *idx, int64_
   }
 }
 
+
+// Rank of this lane among the lanes of the wave holding the same key
+// (valid lanes only), and the size of that group.
+__device__ __forceinline__ void peer_rank(bool valid, int e, int key_bits, int *rank, int *group,
+                                          bool *leader) {
+  const int lane = lane_id();
+  uint64_t peers = __ballot(valid);
+  for (int b = 0; b < key_bits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  *rank = __popcll(peers & lt);
+  *group = __popcll(peers);
+  *leader = valid && (peers >> lane) == 1ull;
+}
+
+// Everything in one work-group (16 waves) for up to kFusedPairs pairs: each
+// wave counts a contiguous slice of the slot-major sequence, the block scans
+// the counts into slice bases, then each wave places its slice in order.
+constexpr int kFusedWaves = 16;
+constexpr int kFusedPairs = kFusedWaves * 512;
+constexpr int kFusedExperts = 256;
+
+__global__ __launch_bounds__(1024) void permute_fused_kernel(
+    const int32_t *idx, int64_t T, int k, int E, int n_shared, int bm, int max_tiles, int key_bits,
+    int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *row_pair, int32_t *inv_perm,
+    int32_t *tiles, int32_t *n_tiles) {
+  __shared__ int cnt[kFusedWaves][kFusedExperts];
+  __shared__ int sh[17];
+  __shared__ int s_off[kFusedExperts + 8];
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  const int64_t P = T * k;
+  const int slice = int((P + kFusedWaves * 64 - 1) / (kFusedWaves * 64)) * 64;
+  for (int i = threadIdx.x; i < kFusedWaves * kFusedExperts; i += blockDim.x) (&cnt[0][0])[i] = 0;
+  __syncthreads();
+  const int64_t p0 = int64_t(w) * slice;
+  for (int it = 0; it < slice; it += 64) {
+    const int64_t p = p0 + it + lane;
+    if (p < P) {
+      int64_t t;
+      int sl;
+      const int e = pair_expert(idx, p, T, k, &t, &sl);
+      if (e >= 0 && e < E) atomicAdd(&cnt[w][e], 1);
+    }
+  }
+  __syncthreads();
+  const int e = threadIdx.x;
+  int c = 0;
+  if (e < E) {
+    for (int ww = 0; ww < kFusedWaves; ++ww) c += cnt[ww][e];
+  } else if (e < E + n_shared) {
+    c = int(T);
+  }
+  const int off = schedule(c, E, n_shared, T, bm, max_tiles, counts, offsets, row_token, tiles, n_tiles, sh,
+                           s_off);
+  if (e < E) {
+    int run = off;
+    for (int ww = 0; ww < kFusedWaves; ++ww) {
+      const int v = cnt[ww][e];
+      cnt[ww][e] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int it = 0; it < slice; it += 64) {
+    const int64_t p = p0 + it + lane;
+    bool valid = p < P;
+    int64_t t = 0;
+    int sl = 0, ex = 0;
+    if (valid) {
+      ex = pair_expert(idx, p, T, k, &t, &sl);
+      valid = ex >= 0 && ex < E;
+      if (!valid) ex = 0;
+    }
+    int rank, group;
+    bool leader;
+    peer_rank(valid, ex, key_bits, &rank, &group, &leader);
+    const int start = valid ? cnt[w][ex] : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (leader) cnt[w][ex] = start + group;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      const int pos = start + rank;
+      const int pair = int(t * k + sl);
+      row_pair[pos] = pair;
+      row_token[pos] = int32_t(t);
+      inv_perm[pair] = pos;
+    }
+  }
+}
+
 }  // namespace moeq
 
 using namespace moeq;
@@ -212,17 +332,22 @@ extern "C" int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
   size_t need = moeq_permute_workspace_size(T, top_k, E, n_shared);
   if (!ws || ws_bytes < need)
     return fail(MOEQ_ERR_WORKSPACE, "permute: workspace %zu < %zu bytes", ws_bytes, need);
-  int32_t *cc = static_cast<int32_t *>(ws);
-  int64_t nchunks = cdiv(T * top_k, kChunk);
   int key_bits = 1;
   while ((1 << key_bits) < E) ++key_bits;
   hipStream_t s = as_stream(stream);
+  const int max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm);
+  if (T * top_k <= kFusedPairs && E + n_shared <= kFusedExperts) {
+    permute_fused_kernel<<<1, 1024, 0, s>>>(idx, T, top_k, E, n_shared, bm, max_tiles, key_bits, counts,
+                                            offsets, row_token, row_pair, inv_perm, tiles, n_tiles);
+    return check_launch("permute/fused");
+  }
+  int32_t *cc = static_cast<int32_t *>(ws);
+  int64_t nchunks = cdiv(T * top_k, kChunk);
   dim3 grid(unsigned(cdiv(nchunks, 4))), block(256);
   size_t lds = size_t(4) * E * sizeof(int32_t);
   hist_kernel<<<grid, block, lds, s>>>(idx, T, top_k, E, nchunks, cc);
   int rc = check_launch("permute/hist");
   if (rc) return rc;
-  const int max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm);
   scan_kernel<<<1, 1024, 0, s>>>(cc, nchunks, T, top_k, E, n_shared, bm, max_tiles, counts,
                                  offsets, row_token, tiles, n_tiles);
   rc = check_launch("permute/scan");

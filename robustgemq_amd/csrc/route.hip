@@ -22,8 +22,9 @@ struct RouteArgs {
   int wg_dtype;
   const float *bias;  // may be null
   int E, k, norm;
-  void *logits;      // may be null
+  void *logits;      // rounded logits [T, E]
   int logits_dtype;  // rounding target of the logits
+  int store_dtype;   // element type of `logits` (logits_dtype, or F32 scratch)
   int32_t *idx;
   float *w;
 };
@@ -130,73 +131,73 @@ __device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
   }
 }
 
-template <int MAXCH, int TT, int EREG>
-__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+// Logits of a TT-token x EE-expert tile per wave.  Lane l runs the TT*EE
+// fused multiply-add chains over its k set (k = 512 i + 8 l + j), then every
+// chain is reduced with the xor butterfly; the order per logit is exactly the
+// one documented at the top of this file whatever the tiling.
+template <int TT, int EE, int MAXCH>
+__global__ __launch_bounds__(256) void logits_kernel(RouteArgs a, int n_et) {
   const int lane = lane_id();
   const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t t0 = wave * TT;
+  const int64_t tt_tile = wave / n_et;
+  const int e0 = int(wave % n_et) * EE;
+  const int64_t t0 = tt_tile * TT;
   if (t0 >= a.T) return;
-
-  float xr[TT][MAXCH][8];
+  float ch[TT][EE];
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-    for (int i = 0; i < MAXCH; ++i) {
-      int k0 = 512 * i + 8 * lane;
-      if (t0 + tt < a.T && k0 < a.H) {
-        load8(a.x, a.x_dtype, (t0 + tt) * a.H + k0, xr[tt][i]);
-      } else {
+    for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xr[tt][i][j] = 0.f;
+  for (int i = 0; i < MAXCH; ++i) {
+    const int k0 = 512 * i + 8 * lane;
+    if (k0 < a.H) {
+      float xv[TT][8], wv[EE][8];
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        if (t0 + tt < a.T) {
+          load8(a.x, a.x_dtype, (t0 + tt) * a.H + k0, xv[tt]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xv[tt][j] = 0.f;
+        }
       }
-    }
-
-  float lg[TT][EREG];
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt)
+      for (int ee = 0; ee < EE; ++ee) {
+        if (e0 + ee < a.E) {
+          load8(a.wg, a.wg_dtype, int64_t(e0 + ee) * a.H + k0, wv[ee]);
+        } else {
 #pragma unroll
-    for (int r = 0; r < EREG; ++r) lg[tt][r] = 0.f;
-
-  for (int e = 0; e < a.E; ++e) {
-    float v[TT];
+          for (int j = 0; j < 8; ++j) wv[ee][j] = 0.f;
+        }
+      }
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) v[tt] = 0.f;
-#pragma unroll
-    for (int i = 0; i < MAXCH; ++i) {
-      int k0 = 512 * i + 8 * lane;
-      if (k0 < a.H) {
-        float wr[8];
-        load8(a.wg, a.wg_dtype, int64_t(e) * a.H + k0, wr);
+      for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[tt] = __builtin_fmaf(xr[tt][i][j], wr[j], v[tt]);
-      }
-    }
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-      float s = v[tt];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) s = s + __shfl_xor(s, o);
-      if (a.bias) s = s + a.bias[e];
-      s = round_logit(s, a.logits_dtype);
-      if ((e & 63) == lane) lg[tt][e >> 6] = s;
+          for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = __builtin_fmaf(xv[tt][j], wv[ee][j], ch[tt][ee]);
     }
   }
-
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) {
-    const int64_t t = t0 + tt;
-    if (t >= a.T) break;
-    if (a.logits) {
+  for (int o = 32; o >= 1; o >>= 1)
 #pragma unroll
-      for (int r = 0; r < EREG; ++r) {
-        int e = 64 * r + lane;
-        if (e < a.E) store_logit(a.logits, a.logits_dtype, t * a.E + e, lg[tt][r]);
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = ch[tt][ee] + __shfl_xor(ch[tt][ee], o);
+  // every lane now holds all TT*EE logits; lane j stores logit j
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int ee = 0; ee < EE; ++ee) {
+      const int64_t t = t0 + tt;
+      const int e = e0 + ee;
+      if (lane == tt * EE + ee && t < a.T && e < a.E) {
+        float v = ch[tt][ee];
+        if (a.bias) v = v + a.bias[e];
+        store_logit(a.logits, a.store_dtype, t * a.E + e, round_logit(v, a.logits_dtype));
       }
     }
-    select_topk<EREG>(lg[tt], a.E, a.k, a.norm, t, a.idx, a.w);
-  }
 }
 
 template <int EREG>
@@ -215,19 +216,33 @@ __global__ __launch_bounds__(256) void topk_from_logits_kernel(
   select_topk<EREG>(vals, E, k, norm, t, idx, w);
 }
 
-template <int MAXCH, int TT>
-static void launch_route_e(const RouteArgs &a, int ereg, hipStream_t s) {
-  int64_t waves = cdiv(a.T, TT);
+static int ereg_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
+
+template <int TT, int EE>
+static void launch_logits(const RouteArgs &a, int maxch, hipStream_t s) {
+  const int n_et = int(cdiv(a.E, EE));
+  const int64_t waves = cdiv(a.T, TT) * n_et;
   dim3 grid(unsigned(cdiv(waves, 4))), block(256);
-  switch (ereg) {
-    case 1: route_kernel<MAXCH, TT, 1><<<grid, block, 0, s>>>(a); break;
-    case 2: route_kernel<MAXCH, TT, 2><<<grid, block, 0, s>>>(a); break;
-    case 4: route_kernel<MAXCH, TT, 4><<<grid, block, 0, s>>>(a); break;
-    default: route_kernel<MAXCH, TT, 8><<<grid, block, 0, s>>>(a); break;
+  switch (maxch) {
+    case 1: logits_kernel<TT, EE, 1><<<grid, block, 0, s>>>(a, n_et); break;
+    case 2: logits_kernel<TT, EE, 2><<<grid, block, 0, s>>>(a, n_et); break;
+    case 4: logits_kernel<TT, EE, 4><<<grid, block, 0, s>>>(a, n_et); break;
+    default: logits_kernel<TT, EE, 8><<<grid, block, 0, s>>>(a, n_et); break;
   }
 }
 
-static int ereg_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
+static int launch_topk(const void *logits, int dtype, int64_t T, int E, int k, int norm, int32_t *idx,
+                       float *w, hipStream_t s) {
+  dim3 grid(unsigned(cdiv(T, 4))), block(256);
+  switch (ereg_for(E)) {
+    case 1: topk_from_logits_kernel<1><<<grid, block, 0, s>>>(logits, dtype, T, E, k, norm, idx, w); break;
+    case 2: topk_from_logits_kernel<2><<<grid, block, 0, s>>>(logits, dtype, T, E, k, norm, idx, w); break;
+    case 4: topk_from_logits_kernel<4><<<grid, block, 0, s>>>(logits, dtype, T, E, k, norm, idx, w); break;
+    default: topk_from_logits_kernel<8><<<grid, block, 0, s>>>(logits, dtype, T, E, k, norm, idx, w); break;
+  }
+  return check_launch("route/topk");
+}
+
 
 static bool valid_dtype(int d) { return d == MOEQ_F16 || d == MOEQ_BF16 || d == MOEQ_F32; }
 
@@ -235,10 +250,16 @@ static bool valid_dtype(int d) { return d == MOEQ_F16 || d == MOEQ_BF16 || d == 
 
 using namespace moeq;
 
+extern "C" size_t moeq_route_workspace_size(int64_t T, int E) {
+  if (T <= 0 || E <= 0) return 0;
+  return align256(size_t(T) * size_t(E) * sizeof(float));
+}
+
 extern "C" int moeq_route(const void *x, int x_dtype, int64_t T, int H,
                           const void *gate_w, int gate_dtype, const float *logit_bias,
                           int E, int top_k, int norm_topk, void *logits_out,
-                          int32_t *idx_out, float *w_out, void *stream) {
+                          int32_t *idx_out, float *w_out, void *ws, size_t ws_bytes,
+                          void *stream) {
   if (!x || !gate_w || !idx_out || !w_out) return fail(MOEQ_ERR_INVALID, "route: null pointer");
   if (!valid_dtype(x_dtype) || !valid_dtype(gate_dtype))
     return fail(MOEQ_ERR_INVALID, "route: dtype x=%d gate=%d", x_dtype, gate_dtype);
@@ -248,19 +269,28 @@ extern "C" int moeq_route(const void *x, int x_dtype, int64_t T, int H,
   if (E <= 0 || E > 512) return fail(MOEQ_ERR_UNSUPPORTED, "route: n_experts=%d not in 1..512", E);
   if (top_k <= 0 || top_k > E || top_k > kMaxTopK)
     return fail(MOEQ_ERR_INVALID, "route: top_k=%d must be in 1..min(n_experts=%d, %d)", top_k, E, kMaxTopK);
+  const int ldt = gate_dtype == MOEQ_F32 ? MOEQ_F32 : x_dtype;
+  void *lg = logits_out;
+  int lg_dt = ldt;
+  if (!lg) {
+    if (!ws || ws_bytes < moeq_route_workspace_size(T, E))
+      return fail(MOEQ_ERR_WORKSPACE, "route: logits_out is NULL and workspace %zu < %zu bytes", ws_bytes,
+                  moeq_route_workspace_size(T, E));
+    lg = ws;  // rounded logits kept as fp32 (exact)
+    lg_dt = MOEQ_F32;
+  }
   RouteArgs a{x, x_dtype, T, H, gate_w, gate_dtype, logit_bias, E, top_k, norm_topk ? 1 : 0,
-              logits_out, gate_dtype == MOEQ_F32 ? MOEQ_F32 : x_dtype, idx_out, w_out};
+              lg, ldt, lg_dt, idx_out, w_out};
   hipStream_t s = as_stream(stream);
-  int ereg = ereg_for(E);
-  if (H <= 512)
-    launch_route_e<1, 8>(a, ereg, s);
-  else if (H <= 1024)
-    launch_route_e<2, 8>(a, ereg, s);
-  else if (H <= 2048)
-    launch_route_e<4, 4>(a, ereg, s);
+  const int maxch = H <= 512 ? 1 : H <= 1024 ? 2 : H <= 2048 ? 4 : 8;
+  if (T <= 2)
+    launch_logits<1, 4>(a, maxch, s);
   else
-    launch_route_e<8, 2>(a, ereg, s);
-  return check_launch("route");
+    launch_logits<4, 4>(a, maxch, s);
+  int rc = check_launch("route/logits");
+  if (rc) return rc;
+  // the selection reads the rounded logits (stored as ldt, or exactly as fp32)
+  return launch_topk(lg, lg_dt, T, E, top_k, norm_topk ? 1 : 0, idx_out, w_out, s);
 }
 
 extern "C" int moeq_route_from_logits(const void *logits, int dtype, int64_t T,
@@ -272,14 +302,5 @@ extern "C" int moeq_route_from_logits(const void *logits, int dtype, int64_t T,
   if (E <= 0 || E > 512) return fail(MOEQ_ERR_UNSUPPORTED, "route_from_logits: n_experts=%d not in 1..512", E);
   if (top_k <= 0 || top_k > E || top_k > kMaxTopK)
     return fail(MOEQ_ERR_INVALID, "route_from_logits: top_k=%d must be in 1..min(n_experts=%d, %d)", top_k, E, kMaxTopK);
-  dim3 grid(unsigned(cdiv(T, 4))), block(256);
-  hipStream_t s = as_stream(stream);
-  int n = norm_topk ? 1 : 0;
-  switch (ereg_for(E)) {
-    case 1: topk_from_logits_kernel<1><<<grid, block, 0, s>>>(logits, dtype, T, E, top_k, n, idx_out, w_out); break;
-    case 2: topk_from_logits_kernel<2><<<grid, block, 0, s>>>(logits, dtype, T, E, top_k, n, idx_out, w_out); break;
-    case 4: topk_from_logits_kernel<4><<<grid, block, 0, s>>>(logits, dtype, T, E, top_k, n, idx_out, w_out); break;
-    default: topk_from_logits_kernel<8><<<grid, block, 0, s>>>(logits, dtype, T, E, top_k, n, idx_out, w_out); break;
-  }
-  return check_launch("route_from_logits");
+  return launch_topk(logits, dtype, T, E, top_k, norm_topk ? 1 : 0, idx_out, w_out, as_stream(stream));
 }

@@ -38,9 +38,11 @@ def route(x, gate_w, top_k, norm_topk, logits=True, logit_bias=None):
     idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
     w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
     bias = None if logit_bias is None else logit_bias.float().contiguous()
+    ws_bytes = 0 if logits else L.lib().moeq_route_workspace_size(T, E)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
     L.check(L.lib().moeq_route(L.ptr(x), L.dtype_code(x.dtype), T, H, L.ptr(gate_w.contiguous()), gdt, L.ptr(bias),
-                               E, top_k,
-                               int(bool(norm_topk)), L.ptr(lg), L.ptr(idx), L.ptr(w), L.stream_handle(dev)),
+                               E, top_k, int(bool(norm_topk)), L.ptr(lg), L.ptr(idx), L.ptr(w), L.ptr(ws), ws_bytes,
+                               L.stream_handle(dev)),
             "moeq_route")
     return lg, idx, w
 
@@ -89,6 +91,8 @@ def grouped_gemm(a, rows, n_out, tiles, n_tiles, max_tiles, bm, p0, p1=None, row
     Returns [rows, N] (or [splits, rows, N] fp32 for split-K)."""
     dev = a.device
     N = p0.N
+    if a.dtype == torch.bfloat16 and bm >= 32:
+        a = a.to(torch.float16)  # LDS-staged tiles read F16 rows (exact for |x| in fp16 range)
     epi = L.EPI_SILU_MUL if p1 is not None else L.EPI_STORE
     shape = (rows, N) if splits == 1 else (splits, rows, N)
     out = torch.empty(shape, dtype=out_dtype, device=dev)

@@ -76,10 +76,13 @@ def test_invalid_arguments_are_rejected_before_launch():
     rc, msg = _err(lib.moeq_prep_scales(fake, fake, 10, 7, fake, None))
     assert rc == -1
     # route: top_k > E, unsupported hidden size
-    rc, msg = _err(lib.moeq_route(fake, L.F16, 4, 2048, fake, L.F16, None, 8, 9, 0, None, fake, fake, None))
+    rc, msg = _err(lib.moeq_route(fake, L.F16, 4, 2048, fake, L.F16, None, 8, 9, 0, None, fake, fake, None, 0, None))
     assert rc == -1 and "top_k" in msg
-    rc, msg = _err(lib.moeq_route(fake, L.F16, 4, 8192, fake, L.F16, None, 8, 2, 0, None, fake, fake, None))
+    rc, msg = _err(lib.moeq_route(fake, L.F16, 4, 8192, fake, L.F16, None, 8, 2, 0, None, fake, fake, None, 0, None))
     assert rc == -2
+    rc, msg = _err(lib.moeq_route(fake, L.F16, 4, 2048, fake, L.F16, None, 8, 2, 0, None, fake, fake, fake,
+                                  lib.moeq_route_workspace_size(4, 8) - 1, None))
+    assert rc == -3 and "workspace" in msg
     # permute: workspace too small
     need = lib.moeq_permute_workspace_size(16, 2, 8, 0)
     rc, msg = _err(lib.moeq_permute(fake, 16, 2, 8, 0, 16, fake, fake, fake, fake, fake, fake, fake, fake,
@@ -130,10 +133,7 @@ def test_max_tiles_bounds_every_routing():
             counts = list(np.bincount(idx.reshape(-1), minlength=E)) + [T] * S
             tiles = 0
             for m in counts:
-                if m:
-                    nmt = -(-m // bm)
-                    rt = -(-(-(-m // nmt)) // 16) * 16
-                    tiles += -(-m // rt)
+                tiles += -(-m // bm)
             assert tiles <= bound, (T, k, E, S, bm, tiles, bound)
         assert permute  # imported for parity of the tile rule with the oracle grouping
 
