@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run one 256 MiB device-to-device copy first (reference size for HBM counters)")
     return ap.parse_args()
 
 
@@ -74,6 +76,13 @@ def main():
     from robustgemq_amd.synthetic import CONFIGS, build_block, flops, make_inputs, make_weights
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # reads and writes exactly 256 MiB
+        torch.cuda.synchronize()
+        del src, dst
     cfg = CONFIGS[args.config]
     T = args.tokens
     log(f"[bench] building {cfg.name} (synthetic weights, seed 0)")

@@ -38,8 +38,9 @@ extern "C" {
 
 /* dequantization conventions (gemq/triton_kernels/utils.py:192-212 vs
  * gemq/quantizers/rtn.py:57-61) */
-#define MOEQ_DQ_HQQ 0    /* w = fp16(fp16(q - z) * s)  (checkpoint / fake-quant weights) */
-#define MOEQ_DQ_AFFINE 1 /* w = fp16(q * s + z')      (GemLite-packed zeros z' = -z*s)  */
+#define MOEQ_DQ_HQQ 0     /* w = fp16(fp16(q - z) * s)  (checkpoint / fake-quant weights) */
+#define MOEQ_DQ_AFFINE 1  /* w = fp16(q * s + z')      (GemLite-packed zeros z' = -z*s)  */
+#define MOEQ_DQ_HQQ_INT 2 /* as MOEQ_DQ_HQQ, one op less; every zero an integer 0..1023 */
 
 /* Bits per code supported by the kernels: 1, 2, 3, 4. */
 
@@ -93,7 +94,9 @@ int moeq_repack(const int32_t *ref_words, int64_t K, int64_t N, int nbits,
                 uint32_t *out, void *stream);
 
 /* Fuse per-group fp16 scale s and zero z ([G, N] each) into half2 dwords:
- * MOEQ_DQ_HQQ -> (s, -z); MOEQ_DQ_AFFINE -> (s, z').  Element-wise.
+ * MOEQ_DQ_HQQ -> (s, -z); MOEQ_DQ_AFFINE -> (s, z');
+ * MOEQ_DQ_HQQ_INT -> (s, -(1024 + z)), exact for integer z in 0..1023 (the
+ * caller checks that).  Element-wise.
  * Replaces the separate scales/zeros loads of dequantize(),
  * gemq/triton_kernels/utils.py:192-212. */
 int moeq_prep_scales(const uint16_t *scales, const uint16_t *zeros,

@@ -164,11 +164,15 @@ def unpack_build(words, nbits, N, K):
 
 def prep_scales(s, z, dq_mode):
     """Per-group (s, z) fp16 arrays of equal shape -> uint32 half2 pairs:
-    HQQ (mode 0): low half s, high half -z; AFFINE (mode 1): s, z'."""
+    HQQ (mode 0): low half s, high half -z; AFFINE (mode 1): s, z';
+    HQQ_INT (mode 2, integer z in 0..1023): s, -(1024 + z)."""
     sb = np.asarray(s, dtype=np.float16).view(np.uint16).astype(np.uint32)
     zz = np.asarray(z, dtype=np.float16)
     if dq_mode == 0:
         zz = -zz
+    elif dq_mode == 2:
+        assert np.all((zz == np.round(zz)) & (zz >= 0) & (zz <= 1023))
+        zz = (-(1024.0 + zz.astype(np.float64))).astype(np.float16)
     zb = zz.astype(np.float16).view(np.uint16).astype(np.uint32)
     return (sb | (zb << 16)).astype(np.uint32)
 

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libmoeq.so")
 
 MOEQ_OK = 0
 F16, BF16, F32 = 0, 1, 2
-DQ_HQQ, DQ_AFFINE = 0, 1
+DQ_HQQ, DQ_AFFINE, DQ_HQQ_INT = 0, 1, 2
 EPI_STORE, EPI_SILU_MUL = 0, 1
 
 c_void_p = ctypes.c_void_p

@@ -14,7 +14,7 @@ static int check_proj(const moeq_proj *p, const char *name) {
   if (p->N <= 0 || p->N % 16) return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: %s N=%d must be a positive multiple of 16", name, p->N);
   if (p->group_size < 32 || p->group_size % 32 || p->K % p->group_size)
     return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: %s group_size=%d must be a multiple of 32 dividing K=%d", name, p->group_size, p->K);
-  if (p->dq_mode != MOEQ_DQ_HQQ && p->dq_mode != MOEQ_DQ_AFFINE)
+  if (p->dq_mode != MOEQ_DQ_HQQ && p->dq_mode != MOEQ_DQ_AFFINE && p->dq_mode != MOEQ_DQ_HQQ_INT)
     return fail(MOEQ_ERR_INVALID, "grouped_gemm: %s dq_mode=%d", name, p->dq_mode);
   return MOEQ_OK;
 }

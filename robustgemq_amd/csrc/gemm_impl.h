@@ -14,9 +14,10 @@
 //   B (weights): each lane loads its own lane slice (`BITS` words = 32 codes of
 //      one column) with one vector load, one chunk ahead, and dequantizes it
 //      in registers straight into the MFMA B-fragment layout:
-//        raw pair | 0x6400 per half = 1024 + q (exact) ; - 1024 -> q (exact)
-//        HQQ:    (q + (-z)) * s   = fp16(fp16(q - z) * s), the fake-quant weight
-//        AFFINE: fma(q, s, z')    = GemLite's q * s + z'
+//        pair of codes ORed into the mantissa of 1024 -> 1024 + q (exact)
+//        HQQ_INT: (v - (1024 + z)) * s = fp16(fp16(q - z) * s), fake-quant weight
+//        HQQ:     ((v - 1024) - z) * s  (same value, any fp16 zero)
+//        AFFINE:  fma(v - 1024, s, z')  = GemLite's q * s + z'
 // The inner loop is branch-free: the wave index is made uniform, columns past
 // N load a valid column and are not stored, rows past the tile load a valid
 // row and are not stored, and the number of active 16-row blocks (MBA) is a
@@ -50,22 +51,40 @@ struct GemmArgs {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// The two codes of MFMA step t, pair d of a lane slice, at bits [0, b) of
-// each 16-bit half (layout written by repack_kernel).
+// (x & m) | c in one instruction (the compiler splits it into two when both
+// constants would need the scalar constant bus).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+  return r;
+}
+
+// fp16 pair (1024 + q_lo, 1024 + q_hi) for MFMA step t, pair d of a lane
+// slice: the two codes sit at the same bit offset of the two 16-bit halves
+// (layout written by repack_kernel) and are ORed into the mantissa of 1024.
 template <int BITS>
-__device__ __forceinline__ uint32_t raw_pair(const uint32_t (&w)[BITS], int t, int d) {
+__device__ __forceinline__ uint32_t magic_pair(const uint32_t (&w)[BITS], int t, int d, uint32_t magic) {
   if constexpr (BITS == 4) {
-    return (w[t] >> (4 * d)) & 0x000f000fu;
+    return and_or(w[t] >> (4 * d), 0x000f000fu, magic);
   } else if constexpr (BITS == 2) {
-    return (w[t >> 1] >> (8 * (t & 1) + 2 * d)) & 0x00030003u;
+    return and_or(w[t >> 1] >> (8 * (t & 1) + 2 * d), 0x00030003u, magic);
   } else if constexpr (BITS == 1) {
-    return (w[0] >> (4 * t + d)) & 0x00010001u;
+    return and_or(w[0] >> (4 * t + d), 0x00010001u, magic);
   } else {
-    return ((w[t >> 1] >> (8 * (t & 1) + 2 * d)) & 0x00030003u) |
-           (((w[2] >> (4 * t + d)) & 0x00010001u) << 2);
+    const uint32_t lo = and_or(w[t >> 1] >> (8 * (t & 1) + 2 * d), 0x00030003u, magic);
+    const int hb = 4 * t + d;  // bit of the high code bit in word 2, moved to bit 2
+    const uint32_t hi = hb >= 2 ? (w[2] >> (hb - 2)) : (w[2] << (2 - hb));
+    return and_or(hi, 0x00040004u, lo);
   }
 }
 
+// B fragment (8 fp16 weights) of MFMA step t from a lane slice and its
+// group's half2 (scale, zero term):
+//   MOEQ_DQ_HQQ_INT: (v + c) * s, c = -(1024 + z)   [z integer in 0..1023]
+//   MOEQ_DQ_HQQ:     ((v - 1024) + (-z)) * s
+//   MOEQ_DQ_AFFINE:  fma(v - 1024, s, z')
+// v - 1024 = q and v + c = q - z are exact, so HQQ modes give
+// fp16(fp16(q - z) * s), the fake-quant weight, and AFFINE GemLite's weight.
 template <int BITS, int DQ>
 __device__ __forceinline__ f16x8 deq_frag(const uint32_t (&w)[BITS], uint32_t sz, int t) {
   const f16 sh = __builtin_bit_cast(f16, uint16_t(sz & 0xffffu));
@@ -75,13 +94,14 @@ __device__ __forceinline__ f16x8 deq_frag(const uint32_t (&w)[BITS], uint32_t sz
   f16x8 r;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    f16x2 v = __builtin_bit_cast(f16x2, raw_pair<BITS>(w, t, d) | 0x64006400u);
-    f16x2 q = v - k1024;
+    const f16x2 v = __builtin_bit_cast(f16x2, magic_pair<BITS>(w, t, d, 0x64006400u));
     f16x2 o;
-    if constexpr (DQ == MOEQ_DQ_HQQ)
-      o = (q + z2) * s2;
+    if constexpr (DQ == MOEQ_DQ_HQQ_INT)
+      o = (v + z2) * s2;
+    else if constexpr (DQ == MOEQ_DQ_HQQ)
+      o = ((v - k1024) + z2) * s2;
     else
-      o = __builtin_elementwise_fma(q, s2, z2);
+      o = __builtin_elementwise_fma(v - k1024, s2, z2);
     r[2 * d] = o[0];
     r[2 * d + 1] = o[1];
   }
@@ -341,14 +361,19 @@ __global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel
   const int c0 = int(blockIdx.z) * g.chunks_per_split;
   const int c1 = min(c0 + g.chunks_per_split, g.nchunks);
   const int bits = g.p[0].nbits[e];
-  const bool hqq = g.dq_mode == MOEQ_DQ_HQQ;
+  const int dq = g.dq_mode;
 #define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D>(g, e, row0, mcount, nt, c0, c1, As)
+#define MOEQ_BITS(B)                                                   \
+  if (dq == MOEQ_DQ_HQQ_INT) MOEQ_TILE(B, MOEQ_DQ_HQQ_INT);           \
+  else if (dq == MOEQ_DQ_HQQ) MOEQ_TILE(B, MOEQ_DQ_HQQ);              \
+  else MOEQ_TILE(B, MOEQ_DQ_AFFINE);
   switch (bits) {
-    case 1: if (hqq) MOEQ_TILE(1, MOEQ_DQ_HQQ); else MOEQ_TILE(1, MOEQ_DQ_AFFINE); break;
-    case 2: if (hqq) MOEQ_TILE(2, MOEQ_DQ_HQQ); else MOEQ_TILE(2, MOEQ_DQ_AFFINE); break;
-    case 3: if (hqq) MOEQ_TILE(3, MOEQ_DQ_HQQ); else MOEQ_TILE(3, MOEQ_DQ_AFFINE); break;
-    default: if (hqq) MOEQ_TILE(4, MOEQ_DQ_HQQ); else MOEQ_TILE(4, MOEQ_DQ_AFFINE); break;
+    case 1: MOEQ_BITS(1) break;
+    case 2: MOEQ_BITS(2) break;
+    case 3: MOEQ_BITS(3) break;
+    default: MOEQ_BITS(4) break;
   }
+#undef MOEQ_BITS
 #undef MOEQ_TILE
 }
 

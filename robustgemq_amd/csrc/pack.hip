@@ -72,6 +72,7 @@ __global__ void prep_scales_kernel(const uint16_t *s, const uint16_t *z,
   if (i >= n) return;
   uint32_t zb = z[i];
   if (mode == MOEQ_DQ_HQQ) zb ^= 0x8000u;  // -z: flip the fp16 sign bit
+  if (mode == MOEQ_DQ_HQQ_INT) zb = f32_to_f16_bits(-(1024.0f + f16_bits_to_f32(uint16_t(zb))));
   out[i] = uint32_t(s[i]) | (zb << 16);
 }
 
@@ -111,7 +112,7 @@ extern "C" int moeq_repack(const int32_t *ref_words, int64_t K, int64_t N,
 extern "C" int moeq_prep_scales(const uint16_t *scales, const uint16_t *zeros,
                                 int64_t n, int dq_mode, uint32_t *out, void *stream) {
   if (!scales || !zeros || !out) return fail(MOEQ_ERR_INVALID, "prep_scales: null pointer");
-  if (dq_mode != MOEQ_DQ_HQQ && dq_mode != MOEQ_DQ_AFFINE)
+  if (dq_mode != MOEQ_DQ_HQQ && dq_mode != MOEQ_DQ_AFFINE && dq_mode != MOEQ_DQ_HQQ_INT)
     return fail(MOEQ_ERR_INVALID, "prep_scales: dq_mode=%d", dq_mode);
   if (n <= 0) return fail(MOEQ_ERR_INVALID, "prep_scales: n=%lld", (long long)n);
   prep_scales_kernel<<<dim3(unsigned(cdiv(n, 256))), dim3(256), 0, as_stream(stream)>>>(

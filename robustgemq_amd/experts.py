@@ -90,6 +90,12 @@ class QuantProjection:
             L.check(lib.moeq_repack(L.ptr(ref_words[e].contiguous()), K, N, self.nbits_list[e], L.ptr(dst), st),
                     "moeq_repack")
         self.word_off = torch.tensor(offs, dtype=torch.int64, device=dev)
+        if dq_mode == L.DQ_HQQ:
+            z = self.zeros
+            if bool(((z == torch.round(z)) & (z >= 0) & (z <= 1023)).all()):
+                # integer zero points: one fp16 op less per weight pair, same weights
+                dq_mode = L.DQ_HQQ_INT
+        self.dq_mode = dq_mode
         self.sz = torch.empty(self.scales.shape, dtype=torch.int32, device=dev)
         L.check(lib.moeq_prep_scales(L.ptr(self.scales), L.ptr(self.zeros), self.scales.numel(), dq_mode,
                                      L.ptr(self.sz), st), "moeq_prep_scales")

@@ -41,11 +41,14 @@ def test_pack_and_repack_bit_exact(device, nbits):
     Kb = 512
     codes_b = codes[:, :Kb]
     wb, _ = ops.pack_weights_over_cols(torch.from_numpy(codes_b).to(device), nbits)
-    proj = QuantProjection([wb], [torch.from_numpy(s[:Kb // 64]).to(device)], [torch.from_numpy(z[:Kb // 64]).to(device)],
-                           [nbits], Kb, N, 64, 0)
-    np.testing.assert_array_equal(to_np(proj.words).view(np.uint32).reshape(Kb // 128, N, 4, nbits),
-                                  oq.repack_build(codes_b, nbits))
-    np.testing.assert_array_equal(to_np(proj.sz).view(np.uint32), oq.prep_scales(s[:Kb // 64], z[:Kb // 64], 0))
+    for zz, want_mode in ((z, 2), (z + np.float16(0.25), 0)):  # integer zeros select the integer mode
+        proj = QuantProjection([wb], [torch.from_numpy(s[:Kb // 64]).to(device)],
+                               [torch.from_numpy(zz[:Kb // 64]).to(device)], [nbits], Kb, N, 64, 0)
+        assert proj.dq_mode == want_mode
+        np.testing.assert_array_equal(to_np(proj.words).view(np.uint32).reshape(Kb // 128, N, 4, nbits),
+                                      oq.repack_build(codes_b, nbits))
+        np.testing.assert_array_equal(to_np(proj.sz).view(np.uint32),
+                                      oq.prep_scales(s[:Kb // 64], zz[:Kb // 64], want_mode))
 
 
 # ------------------------------------------------------------------ routing
@@ -115,16 +118,19 @@ def test_permute_bit_exact(device, T, k, E, S, bm):
 
 # ------------------------------------------------------------- grouped GEMM
 def _make_proj(device, rng, E, K, N, bits, g, mode):
+    """mode: 'int' (integer HQQ zeros), 'frac' (fractional HQQ zeros, as GPTQ
+    checkpoints have) or 'affine' (GemLite zeros z' = -z*s)."""
+    from robustgemq_amd import _lib as L
     from robustgemq_amd.experts import QuantProjection, pack_codes
     codes, s_l, z_l, words = [], [], [], []
     for e in range(E):
         b = bits[e]
         c = rng.integers(0, 1 << b, size=(N, K)).astype(np.uint8)
         s = (np.abs(rng.standard_normal((K // g, N))) * 0.01 + 1e-3).astype(np.float16)
-        if mode == 0:
+        if mode == "int":
             z = rng.integers(0, 1 << b, size=(K // g, N)).astype(np.float16)
-            if b == 1:
-                z[:] = 0.5
+        elif mode == "frac":
+            z = (rng.random((K // g, N)) * ((1 << b) - 1)).astype(np.float16)
         else:
             z = (rng.standard_normal((K // g, N)) * 0.02).astype(np.float16)
         codes.append(c)
@@ -132,10 +138,12 @@ def _make_proj(device, rng, E, K, N, bits, g, mode):
         z_l.append(z)
         words.append(pack_codes(torch.from_numpy(c).to(device), b))
     proj = QuantProjection(words, [torch.from_numpy(s).to(device) for s in s_l],
-                           [torch.from_numpy(z).to(device) for z in z_l], bits, K, N, g, mode)
+                           [torch.from_numpy(z).to(device) for z in z_l], bits, K, N, g,
+                           L.DQ_AFFINE if mode == "affine" else L.DQ_HQQ)
+    assert proj.dq_mode == {"int": L.DQ_HQQ_INT, "frac": L.DQ_HQQ, "affine": L.DQ_AFFINE}[mode]
     dense = []
     for c, s, z in zip(codes, s_l, z_l):
-        if mode == 0:
+        if mode != "affine":
             W = oq.kernel_dequant_hqq(c, s, z, g)  # [K, N] fp16, == fake-quant weight
         else:
             gi = np.arange(K) // g
@@ -145,12 +153,12 @@ def _make_proj(device, rng, E, K, N, bits, g, mode):
 
 
 @pytest.mark.parametrize("bm", [16, 32, 64, 128])
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", ["int", "frac", "affine"])
 @pytest.mark.parametrize("g", [64, 128])
 def test_grouped_gemm_store_matches_fp32(device, bm, mode, g):
     from robustgemq_amd import ops
     _say(f"[gemm/store] bm={bm} mode={mode} g={g}")
-    rng = np.random.default_rng(bm + 10 * mode + g)
+    rng = np.random.default_rng(bm + 10 * len(mode) + g)
     E, K, N = 5, 384, 160  # N not a multiple of the column tile
     bits = [1, 2, 3, 4, 2]
     proj, dense = _make_proj(device, rng, E, K, N, bits, g, mode)
@@ -186,8 +194,8 @@ def test_grouped_gemm_silu_mul_and_splitk(device, bm, adt):
     rng = np.random.default_rng(bm)
     E, K, N = 3, 512, 256
     bits = [2, 3, 4]
-    p1, d1 = _make_proj(device, rng, E, K, N, bits, 64, 0)
-    p3, d3 = _make_proj(device, rng, E, K, N, bits, 64, 0)
+    p1, d1 = _make_proj(device, rng, E, K, N, bits, 64, "int")
+    p3, d3 = _make_proj(device, rng, E, K, N, bits, 64, "int")
     counts = [40, 7, 130]
     rows = sum(counts)
     x = torch.from_numpy((rng.standard_normal((rows, K)) * 0.5).astype(np.float32)).to(adt)
