@@ -176,6 +176,8 @@ typedef struct moeq_gemm {
 /* One launch over every row tile of every expert:
  * out[r, :] = epilogue(A[row_src[r], :] @ deq(W[expert(r)])).
  * p1 must be NULL for MOEQ_EPI_STORE and match p0's layout for SILU_MUL.
+ * Every A row the tiles address (row_src[r], or r) must start below 2 GiB
+ * from a (32-bit row offsets); one expert's packed words must be < 2 GiB.
  * Replaces the per-expert launches of dequant_group_gemm_triton
  * (gemq/triton_kernels/dequant_group_gemm.py:155-202, called once per hit
  * expert at gemq/inference/moe_block.py:766-777), dequant_gemm_triton

@@ -132,6 +132,10 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
   if (T <= 0) return fail(MOEQ_ERR_INVALID, "moe: T=%lld", (long long)T);
   if (out_dtype != m->act_dtype && out_dtype != MOEQ_F32)
     return fail(MOEQ_ERR_INVALID, "moe: out_dtype=%d must be act_dtype or F32", out_dtype);
+  // the LDS-staged GEMM tiles address activation rows with 32-bit offsets
+  if (T * int64_t(m->hidden) * 2 >= (int64_t(1) << 31) ||
+      T * int64_t(m->top_k + m->n_shared) * m->inter * 2 >= (int64_t(1) << 31))
+    return fail(MOEQ_ERR_UNSUPPORTED, "moe: T=%lld too large (activations must stay below 2 GiB)", (long long)T);
   const Plan p = make_plan(m, T);
   if (!ws || ws_bytes < p.total)
     return fail(MOEQ_ERR_WORKSPACE, "moe: workspace %zu < %zu bytes", ws_bytes, p.total);

@@ -14,6 +14,9 @@ static int check_proj(const moeq_proj *p, const char *name) {
   if (p->N <= 0 || p->N % 16) return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: %s N=%d must be a positive multiple of 16", name, p->N);
   if (p->group_size < 32 || p->group_size % 32 || p->K % p->group_size)
     return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: %s group_size=%d must be a multiple of 32 dividing K=%d", name, p->group_size, p->K);
+  if (int64_t(p->K) * p->N / 2 >= (int64_t(1) << 31))
+    return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: %s K*N=%lld too large (one expert's words must stay below 2 GiB)",
+                name, (long long)(int64_t(p->K) * p->N));
   if (p->dq_mode != MOEQ_DQ_HQQ && p->dq_mode != MOEQ_DQ_AFFINE && p->dq_mode != MOEQ_DQ_HQQ_INT)
     return fail(MOEQ_ERR_INVALID, "grouped_gemm: %s dq_mode=%d", name, p->dq_mode);
   return MOEQ_OK;
@@ -54,6 +57,7 @@ extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
   g.K = p0->K;
   g.N = p0->N;
   g.group_size = p0->group_size;
+  g.gshift = (p0->group_size & (p0->group_size - 1)) ? -1 : __builtin_ctz(unsigned(p0->group_size));
   g.dq_mode = p0->dq_mode;
   g.p[0] = ProjDev{p0->words, p0->word_off, p0->sz, p0->sz_off, p0->nbits};
   g.p[1] = p1 ? ProjDev{p1->words, p1->word_off, p1->sz, p1->sz_off, p1->nbits} : g.p[0];
@@ -70,7 +74,8 @@ extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
     case 32: return launch_grouped_gemm<32>(g, silu, gm->a_dtype, gm->out_dtype, mt, sp, s);
     case 64: return launch_grouped_gemm<64>(g, silu, gm->a_dtype, gm->out_dtype, mt, sp, s);
     case 128: return launch_grouped_gemm<128>(g, silu, gm->a_dtype, gm->out_dtype, mt, sp, s);
-    default: return fail(MOEQ_ERR_INVALID, "grouped_gemm: bm=%d not in {16, 32, 64, 128}", gm->bm);
+    case 256: return launch_grouped_gemm<256>(g, silu, gm->a_dtype, gm->out_dtype, mt, sp, s);
+    default: return fail(MOEQ_ERR_INVALID, "grouped_gemm: bm=%d not in {16, 32, 64, 128, 256}", gm->bm);
   }
 }
 
@@ -88,6 +93,7 @@ extern "C" int moeq_gemm_tile_n(int bm, int epilogue) {
     case 32: return tile_n<32>(silu);
     case 64: return tile_n<64>(silu);
     case 128: return tile_n<128>(silu);
+    case 256: return tile_n<256>(silu);
     default: return 0;
   }
 }

@@ -8,7 +8,7 @@
 // needed.  A block has NW waves; wave w owns NB * 16 output columns and all
 // active rows of the tile.  Per 128-deep K chunk:
 //   A (activations, gathered rows): BM >= 32 -> copied global -> LDS with
-//      global_load_lds_dwordx4 (no register staging), 16-byte units XOR-
+//      buffer_load_dwordx4 ... lds (no register staging), 16-byte units XOR-
 //      swizzled by row so the 16 rows of one MFMA fragment hit disjoint banks;
 //      BM == 16 -> loaded straight into registers (decode shapes).
 //   B (weights): each lane loads its own lane slice (`BITS` words = 32 codes of
@@ -42,7 +42,7 @@ struct GemmArgs {
   const int32_t *row_src;
   const int32_t *tiles;
   const int32_t *n_tiles;
-  int K, N, group_size, dq_mode;
+  int K, N, group_size, gshift, dq_mode;  // gshift = log2(group_size), or -1
   ProjDev p[2];
   void *out;
   int64_t ldo, split_stride;
@@ -86,22 +86,26 @@ __device__ __forceinline__ uint32_t magic_pair(const uint32_t (&w)[BITS], int t,
 // v - 1024 = q and v + c = q - z are exact, so HQQ modes give
 // fp16(fp16(q - z) * s), the fake-quant weight, and AFFINE GemLite's weight.
 template <int BITS, int DQ>
-__device__ __forceinline__ f16x8 deq_frag(const uint32_t (&w)[BITS], uint32_t sz, int t) {
+__device__ __forceinline__ f16x2 deq_pair(const uint32_t (&w)[BITS], uint32_t sz, int t, int d) {
   const f16 sh = __builtin_bit_cast(f16, uint16_t(sz & 0xffffu));
   const f16 zh = __builtin_bit_cast(f16, uint16_t(sz >> 16));
   const f16x2 s2 = {sh, sh}, z2 = {zh, zh};
   const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+  const f16x2 v = __builtin_bit_cast(f16x2, magic_pair<BITS>(w, t, d, 0x64006400u));
+  if constexpr (DQ == MOEQ_DQ_HQQ_INT)
+    return (v + z2) * s2;
+  else if constexpr (DQ == MOEQ_DQ_HQQ)
+    return ((v - k1024) + z2) * s2;
+  else
+    return __builtin_elementwise_fma(v - k1024, s2, z2);
+}
+
+template <int BITS, int DQ>
+__device__ __forceinline__ f16x8 deq_frag(const uint32_t (&w)[BITS], uint32_t sz, int t) {
   f16x8 r;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const f16x2 v = __builtin_bit_cast(f16x2, magic_pair<BITS>(w, t, d, 0x64006400u));
-    f16x2 o;
-    if constexpr (DQ == MOEQ_DQ_HQQ_INT)
-      o = (v + z2) * s2;
-    else if constexpr (DQ == MOEQ_DQ_HQQ)
-      o = ((v - k1024) + z2) * s2;
-    else
-      o = __builtin_elementwise_fma(v - k1024, s2, z2);
+    const f16x2 o = deq_pair<BITS, DQ>(w, sz, t, d);
     r[2 * d] = o[0];
     r[2 * d + 1] = o[1];
   }
@@ -147,7 +151,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, int MBA>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, int mcount, int nt,
-                                          int c0, int c1, uint4 (*As)[BM][16]) {
+                                          int c0, int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {
   constexpr int NT = NW * 64;
   static_assert(MBA * 16 <= BM, "active row blocks exceed the tile");
   const int lane = lane_id();
@@ -156,17 +160,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
   const int N = g.N;
   const int n_wave = nt * (NW * NB * 16) + wave * NB * 16;
 
-  const uint32_t *wbase[NP];
-  const uint32_t *sbase[NP];
+  // Expert bases are wave-uniform; each lane adds 32-bit byte offsets (one
+  // expert's words and scales stay far below 2 GiB).
+  const char *wbase[NP];
+  const char *sbase[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    wbase[p] = g.p[p].words + g.p[p].word_off[e];
-    sbase[p] = g.p[p].sz + g.p[p].sz_off[e];
+    wbase[p] = reinterpret_cast<const char *>(g.p[p].words + g.p[p].word_off[e]);
+    sbase[p] = reinterpret_cast<const char *>(g.p[p].sz + g.p[p].sz_off[e]);
   }
   // columns past N read column N - 1 and are never stored
-  int ncol[NB];
+  uint32_t woff[NB], soff[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) ncol[nb] = min(n_wave + nb * 16 + l16, N - 1);
+  for (int nb = 0; nb < NB; ++nb) {
+    const int ncol = min(n_wave + nb * 16 + l16, N - 1);
+    woff[nb] = uint32_t((ncol * 4 + kb) * BITS * 4);
+    soff[nb] = uint32_t(ncol * 4);
+  }
+  const int64_t chunk_bytes = int64_t(N) * 16 * BITS;  // words of one 128-deep chunk
+  const uint32_t grp_bytes = uint32_t(N) * 4u;         // one scale/zero row
 
   f32x4 acc[NP][MBA][NB];
 #pragma unroll
@@ -179,14 +191,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
   uint32_t wcur[NP][NB][BITS], wnxt[NP][NB][BITS];
   uint32_t scur[NP][NB], snxt[NP][NB];
   auto load_b = [&](int c, uint32_t (&w)[NP][NB][BITS], uint32_t (&s)[NP][NB]) {
-    const int grp = (c * 128 + 32 * kb) / g.group_size;
+    const int k = c * 128 + 32 * kb;
+    const uint32_t grp = uint32_t(g.gshift >= 0 ? k >> g.gshift : k / g.group_size);
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+    for (int p = 0; p < NP; ++p) {
+      const char *wc = wbase[p] + int64_t(c) * chunk_bytes;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        load_slice<BITS>(wbase[p] + ((int64_t(c) * N + ncol[nb]) * 4 + kb) * BITS, w[p][nb]);
-        s[p][nb] = sbase[p][int64_t(grp) * N + ncol[nb]];
+        load_slice<BITS>(reinterpret_cast<const uint32_t *>(wc + woff[nb]), w[p][nb]);
+        s[p][nb] = *reinterpret_cast<const uint32_t *>(sbase[p] + (grp * grp_bytes + soff[nb]));
       }
+    }
   };
   auto advance = [&]() {
 #pragma unroll
@@ -218,10 +233,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
       load_b(c0, wcur, scur);
     }
     for (int c = c0; c < c1; ++c) {
-      if (c + 1 < c1) {
-        load_a(c + 1, anxt);
-        load_b(c + 1, wnxt, snxt);
-      }
+      // The next chunk is fetched unconditionally (the last chunk re-reads
+      // itself): a conditional fetch joins two paths, and the wait counts
+      // merged at the join would then wait for the fetch just issued.
+      const int cn = min(c + 1, c1 - 1);
+      load_a(cn, anxt);
+      load_b(cn, wnxt, snxt);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const f16x8 A = to_f16x8<ADT>(acur[t]);
@@ -233,16 +250,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
             acc[p][0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[p][0][nb], 0, 0, 0);
           }
       }
-      if (c + 1 < c1) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acur[t] = anxt[t];
-        advance();
-      }
+      for (int t = 0; t < 4; ++t) acur[t] = anxt[t];
+      advance();
     }
   } else {
-    // ---------------- prefill shapes: A copied global -> LDS, double buffered.
-    // Unit u (16 bytes) of row r lives at As[buf][r][u ^ (r & 15)]; one
-    // global_load_lds_dwordx4 writes 64 consecutive units (4 rows).
+    // ---------------- prefill shapes: A copied global -> LDS, double buffered
+    // in two separate arrays.  Unit u (16 bytes) of row r lives at
+    // A[r][u ^ (r & 15)]; one buffer_load_dwordx4 ... lds writes 64
+    // consecutive units (4 rows).  The chunk loop is unrolled by two so every
+    // LDS access names its buffer at compile time: the copy into one buffer
+    // then never makes the fragment reads of the other wait for it.
     constexpr int UNITS = MBA * 16 * 16;
     constexpr int SEGS = UNITS / NT;
     static_assert(SEGS >= 1 && UNITS % NT == 0, "A staging split");
@@ -256,25 +274,24 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
       const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
       aoff[j] = uint32_t((src * g.lda + u * 8) * 2);
     }
-    auto load_a = [&](int c, int buf) {
+    // Buffer loads take the lane's 32-bit offset plus the chunk's scalar
+    // offset, so no per-lane 64-bit addresses are kept.
+    const __amdgpu_buffer_rsrc_t arsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(abytes), (short)0, 0x7fffffff, 0x00020000);
+    auto load_a = [&](int c, uint4 (*dstA)[16]) {
 #pragma unroll
       for (int j = 0; j < SEGS; ++j) {
-        char *dst = reinterpret_cast<char *>(&As[buf][0][0]) + (j * NW + wave) * 64 * 16;
-        __builtin_amdgcn_global_load_lds(abytes + aoff[j] + uint32_t(c) * 256u, (lds_void *)dst, 16, 0, 0);
+        char *dst = reinterpret_cast<char *>(&dstA[0][0]) + (j * NW + wave) * 64 * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void *)dst, 16, aoff[j], uint32_t(c) * 256u, 0, 0);
       }
     };
-    if (c0 < c1) {
-      load_a(c0, 0);
-      load_b(c0, wcur, scur);
-    }
-    __syncthreads();
-    for (int c = c0; c < c1; ++c) {
-      const int buf = (c - c0) & 1;
-      const bool more = c + 1 < c1;
-      if (more) {
-        load_a(c + 1, buf ^ 1);
-        load_b(c + 1, wnxt, snxt);
-      }
+    auto chunk = [&](int c, uint4 (*Ard)[16], uint4 (*Awr)[16]) {
+      // Fetch the next chunk unconditionally (the last chunk re-reads
+      // itself into the idle buffer): a conditional fetch joins two paths,
+      // and the wait counts merged at the join would wait for it at once.
+      const int cn = min(c + 1, c1 - 1);
+      load_a(cn, Awr);
+      load_b(cn, wnxt, snxt);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         f16x8 B[NP][NB];
@@ -284,8 +301,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
           for (int nb = 0; nb < NB; ++nb) B[p][nb] = deq_frag<BITS, DQ>(wcur[p][nb], scur[p][nb], t);
 #pragma unroll
         for (int mb = 0; mb < MBA; ++mb) {
-          const int r = mb * 16 + l16;
-          const f16x8 A = __builtin_bit_cast(f16x8, As[buf][r][(4 * kb + t) ^ l16]);
+          const f16x8 A = __builtin_bit_cast(f16x8, Ard[mb * 16 + l16][(4 * kb + t) ^ l16]);
 #pragma unroll
           for (int p = 0; p < NP; ++p)
 #pragma unroll
@@ -293,56 +309,83 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
               acc[p][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[p][nb], acc[p][mb][nb], 0, 0, 0);
         }
       }
-      if (more) advance();
+      advance();
       __syncthreads();
+    };
+    if (c0 < c1) {
+      load_a(c0, As0);
+      load_b(c0, wcur, scur);
+    }
+    __syncthreads();
+    for (int c = c0; c < c1; c += 2) {
+      chunk(c, As0, As1);
+      if (c + 1 < c1) chunk(c + 1, As1, As0);
     }
   }
 
-  // ---------------- epilogue: D[row = 4 * (lane / 16) + i][col = lane % 16]
-  char *obytes = static_cast<char *>(g.out);
-  const int split = blockIdx.z;
+  // ---------------- epilogue: D[row = 16 mb + 4 (lane / 16) + i][col = lane % 16].
+  // Each output row starts at a wave-uniform (scalar) address; the lane adds
+  // a 32-bit offset.  Column blocks past N are skipped per wave (N % 16 == 0)
+  // and only the tile's partial last row block tests rows per lane.
+  constexpr int OES = (EPI == MOEQ_EPI_SILU_MUL || ODT != MOEQ_F32) ? 2 : 4;
+  const int64_t ldo_b = g.ldo * OES;
+  char *const tile_out =
+      static_cast<char *>(g.out) + (int64_t(blockIdx.z) * g.split_stride + int64_t(row0) * g.ldo) * OES;
+  const uint32_t lane_off = uint32_t(4 * kb) * uint32_t(ldo_b) + uint32_t((n_wave + l16) * OES);
+  auto put = [&](int mb, int nb, int i) {
+    char *p = tile_out + int64_t(16 * mb + i) * ldo_b + (lane_off + uint32_t(nb * 16 * OES));
+    if constexpr (EPI == MOEQ_EPI_SILU_MUL) {
+      *reinterpret_cast<uint16_t *>(p) = f32_to_f16_bits(silu_mul(acc[0][mb][nb][i], acc[NP - 1][mb][nb][i]));
+    } else if constexpr (ODT == MOEQ_F32) {
+      *reinterpret_cast<float *>(p) = acc[0][mb][nb][i];
+    } else {
+      *reinterpret_cast<uint16_t *>(p) = f32_to_f16_bits(acc[0][mb][nb][i]);
+    }
+  };
 #pragma unroll
-  for (int mb = 0; mb < MBA; ++mb)
+  for (int mb = 0; mb < MBA; ++mb) {
+    if (16 * (mb + 1) <= mcount) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int col = n_wave + nb * 16 + l16;
+      for (int nb = 0; nb < NB; ++nb) {
+        if (n_wave + nb * 16 >= N) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = mb * 16 + 4 * kb + i;
-        if (r >= mcount || col >= N) continue;
-        const int64_t o = int64_t(row0 + r) * g.ldo + col;
-        if constexpr (EPI == MOEQ_EPI_SILU_MUL) {
-          const float h = silu_mul(acc[0][mb][nb][i], acc[NP - 1][mb][nb][i]);
-          reinterpret_cast<uint16_t *>(obytes)[o] = f32_to_f16_bits(h);
-        } else if constexpr (ODT == MOEQ_F32) {
-          reinterpret_cast<float *>(obytes)[split * g.split_stride + o] = acc[0][mb][nb][i];
-        } else {
-          reinterpret_cast<uint16_t *>(obytes)[split * g.split_stride + o] = f32_to_f16_bits(acc[0][mb][nb][i]);
-        }
+        for (int i = 0; i < 4; ++i) put(mb, nb, i);
+      }
+    } else if (16 * mb < mcount) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (n_wave + nb * 16 >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (16 * mb + 4 * kb + i < mcount) put(mb, nb, i);
       }
     }
+  }
 }
 
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ>
 __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0, int mcount, int nt, int c0,
-                                              int c1, uint4 (*As)[BM][16]) {
+                                              int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {
   const int mb_act = (mcount + 15) >> 4;
-#define MOEQ_T(M) gemm_tile<BM, NW, NB, NP, EPI, ADT, ODT, BITS, DQ, M>(g, e, row0, mcount, nt, c0, c1, As)
+#define MOEQ_T(M) gemm_tile<BM, NW, NB, NP, EPI, ADT, ODT, BITS, DQ, M>(g, e, row0, mcount, nt, c0, c1, As0, As1)
   if constexpr (BM == 16) {
     MOEQ_T(1);
   } else if constexpr (BM == 32) {
     MOEQ_T(2);
   } else if constexpr (BM == 64) {
     if (mb_act <= 2) MOEQ_T(2); else MOEQ_T(4);
-  } else {
+  } else if constexpr (BM == 128) {
     if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else MOEQ_T(8);
+  } else {
+    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else if (mb_act <= 8) MOEQ_T(8); else MOEQ_T(16);
   }
 #undef MOEQ_T
 }
 
-// Two work-groups per CU for the LDS-staged shapes (2 waves per SIMD).
+// Two work-groups per CU for the 32..128-row shapes and one 8-wave group for
+// the 256-row shape (its two A buffers take 128 KB of LDS): 2 waves per SIMD.
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT>
-__global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
   // The grid is sized for the host-side bound on row tiles; blocks past the
   // real count (read from the device schedule) exit together.  Work-groups
   // are dealt to the 8 XCDs round-robin, so the live ones are renumbered to
@@ -355,14 +398,15 @@ __global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel
   const unsigned L = b < V8 ? (b & 7u) * (V8 >> 3) + (b >> 3) : b;
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
-  __shared__ uint4 As[BM == 16 ? 1 : 2][BM][16];
+  __shared__ uint4 As0[BM == 16 ? 1 : BM][16];
+  __shared__ uint4 As1[BM == 16 ? 1 : BM][16];
   const int32_t *tp = g.tiles + 4 * mt;
   const int e = tp[0], row0 = tp[1], mcount = tp[2];
   const int c0 = int(blockIdx.z) * g.chunks_per_split;
   const int c1 = min(c0 + g.chunks_per_split, g.nchunks);
   const int bits = g.p[0].nbits[e];
   const int dq = g.dq_mode;
-#define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D>(g, e, row0, mcount, nt, c0, c1, As)
+#define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D>(g, e, row0, mcount, nt, c0, c1, As0, As1)
 #define MOEQ_BITS(B)                                                   \
   if (dq == MOEQ_DQ_HQQ_INT) MOEQ_TILE(B, MOEQ_DQ_HQQ_INT);           \
   else if (dq == MOEQ_DQ_HQQ) MOEQ_TILE(B, MOEQ_DQ_HQQ);              \
@@ -389,6 +433,10 @@ template <> struct Shape<64, true> { static constexpr int NW = 4, NB = 2; };
 template <> struct Shape<64, false> { static constexpr int NW = 4, NB = 4; };
 template <> struct Shape<128, true> { static constexpr int NW = 4, NB = 2; };
 template <> struct Shape<128, false> { static constexpr int NW = 4, NB = 4; };
+// 256-row tiles: 8 waves, each with all rows and 16 (gate + up) or 32 columns,
+// so one dequantized B fragment feeds 16 row blocks.
+template <> struct Shape<256, true> { static constexpr int NW = 8, NB = 1; };
+template <> struct Shape<256, false> { static constexpr int NW = 8, NB = 2; };
 
 // Launches one configuration (defined in gemm_bm<BM>.hip).
 template <int BM>

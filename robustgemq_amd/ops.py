@@ -214,7 +214,7 @@ def _proj_from_stacked(wq, scales, zeros, nbits, wq_strides, zs_strides, K, grou
 
 
 def _bm_for(m):
-    return 16 if m <= 16 else 32 if m <= 32 else 64 if m <= 64 else 128
+    return 16 if m <= 16 else 32 if m <= 32 else 64 if m <= 64 else 128 if m < 192 else 256
 
 
 def _slot_tiles(expert_ids, rows_per_slot, bm):

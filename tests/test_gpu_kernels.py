@@ -152,7 +152,7 @@ def _make_proj(device, rng, E, K, N, bits, g, mode):
     return proj, dense
 
 
-@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+@pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("mode", ["int", "frac", "affine"])
 @pytest.mark.parametrize("g", [64, 128])
 def test_grouped_gemm_store_matches_fp32(device, bm, mode, g):
@@ -186,7 +186,7 @@ def test_grouped_gemm_store_matches_fp32(device, bm, mode, g):
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("bm", [16, 128])
+@pytest.mark.parametrize("bm", [16, 128, 256])
 @pytest.mark.parametrize("adt", [torch.float16, torch.bfloat16])
 def test_grouped_gemm_silu_mul_and_splitk(device, bm, adt):
     from robustgemq_amd import ops

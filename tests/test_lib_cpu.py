@@ -155,6 +155,7 @@ def test_layer_plan_and_workspace():
     m.w2 = _proj(1024, 1024)
     assert lib.moeq_moe_workspace_size(m, 2048) == 0  # invalid layer -> 0
     assert lib.moeq_gemm_tile_n(128, L.EPI_SILU_MUL) > 0 and lib.moeq_gemm_tile_n(48, 0) == 0
+    assert lib.moeq_gemm_tile_n(256, L.EPI_SILU_MUL) == 128 and lib.moeq_gemm_tile_n(256, L.EPI_STORE) == 256
 
 
 @pytest.mark.parametrize("nbits", [1, 2, 3, 4])
