@@ -84,14 +84,6 @@ __device__ int block_exclusive_scan(int v, int *sh, int *total) {
   return r;
 }
 
-// Row tiles of an expert with m rows: full bm-row tiles and one remainder
-// tile (the GEMM rounds a tile's active rows up to 2, 4 or 8 blocks of 16);
-// returns the count, *rt the tile height.
-__device__ __forceinline__ int tiles_of(int m, int bm, int *rt) {
-  *rt = bm;
-  return m <= 0 ? 0 : (m + bm - 1) / bm;
-}
-
 // Given per-expert row counts (one per thread e < Et), writes counts,
 // offsets, the tile schedule and the shared-expert rows; returns this
 // expert's first row.  Every thread of the block must call it.
@@ -99,11 +91,13 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
                         int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *tiles,
                         int32_t *n_tiles, int *sh, int *s_off) {
   const int e = threadIdx.x, Et = E + n_shared;
-  int rt;
-  const int nt = e < Et ? tiles_of(c, bm, &rt) : 0;
-  int tot_rows, tot_tiles;
-  const int off = block_exclusive_scan(e < Et ? c : 0, sh, &tot_rows);
-  const int tb = block_exclusive_scan(nt, sh, &tot_tiles);
+  const int m = e < Et ? c : 0;
+  const int nfull = m / bm, npart = m % bm ? 1 : 0;
+  int tot_rows, tot_full, tot_part;
+  const int off = block_exclusive_scan(m, sh, &tot_rows);
+  const int tb = block_exclusive_scan(nfull, sh, &tot_full);
+  const int tp0 = tot_full + block_exclusive_scan(npart, sh, &tot_part);
+  const int tot_tiles = tot_full + tot_part;
   if (e < Et) {
     counts[e] = c;
     offsets[e] = off;
@@ -115,12 +109,21 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
     // a corrupted idx from writing past the schedule buffer
     *n_tiles = min(tot_tiles, max_tiles);
   }
-  for (int j = 0; j < nt && tb + j < max_tiles; ++j) {
-    const int r0 = j * rt;
+  // Every expert's full tiles come first and the remainder tiles last: the
+  // GEMM work-groups are dispatched in tile order, so the long tiles start
+  // first and the short ones fill the tail of the launch.
+  for (int j = 0; j < nfull && tb + j < max_tiles; ++j) {
     int32_t *tp = tiles + 4 * (tb + j);
     tp[0] = e;
-    tp[1] = off + r0;
-    tp[2] = min(rt, c - r0);
+    tp[1] = off + j * bm;
+    tp[2] = bm;
+    tp[3] = 0;
+  }
+  if (npart && tp0 < max_tiles) {
+    int32_t *tp = tiles + 4 * tp0;
+    tp[0] = e;
+    tp[1] = off + nfull * bm;
+    tp[2] = m - nfull * bm;
     tp[3] = 0;
   }
   __syncthreads();
