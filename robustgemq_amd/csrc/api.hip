@@ -43,16 +43,8 @@ static Plan make_plan(const moeq_moe *m, int64_t T) {
   const double avg = double(p.pairs) / double(m->n_experts);
   p.bm = avg <= 16 ? 16 : avg <= 32 ? 32 : avg <= 64 ? 64 : 128;
   p.max_tiles = moeq_max_tiles(T, m->top_k, m->n_experts, m->n_shared, p.bm);
-  // Down projection: few live blocks (decode) -> split K over fp32 slices.
+  // 16-row (decode) blocks already split K over their waves
   p.splits = 1;
-  if (p.bm == 16) {
-    const int64_t bn = moeq_gemm_tile_n(16, MOEQ_EPI_STORE);
-    const int64_t live = std::min<int64_t>(p.max_tiles, p.pairs + int64_t(m->n_shared)) *
-                         cdiv(m->hidden, bn);
-    const int64_t want = 1024;
-    int64_t s = cdiv(want, std::max<int64_t>(live, 1));
-    p.splits = int(std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(s, 8), m->inter / 128)));
-  }
   p.y_dtype = p.splits > 1 ? MOEQ_F32 : MOEQ_F16;
   const int Et = m->n_experts + m->n_shared;
   size_t o = 0;

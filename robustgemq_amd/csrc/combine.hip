@@ -1,6 +1,6 @@
 // Top-k weighted combine of the grouped expert outputs (plus shared experts).
-// One work-group per token, 8 columns per thread, fixed summation order
-// (slots ascending, split-K slices ascending), no atomics: bit-reproducible.
+// 8 columns per thread, fixed summation order (slots ascending, split-K
+// slices ascending), no atomics: bit-reproducible.
 #include <algorithm>
 
 #include "common.h"
@@ -25,57 +25,62 @@ __device__ __forceinline__ void load_y8(const void *y, int64_t off, float (&v)[8
   }
 }
 
+// One 64-thread block per (token, 512-column block); each thread sums 8
+// columns over the token's slots in slot order (split-K slices in order).
 template <int YDT>
-__global__ __launch_bounds__(256) void combine_kernel(
+__global__ __launch_bounds__(64) void combine_kernel(
     const void *y, int splits, int64_t split_stride, int64_t ldy, const int32_t *inv_perm,
     const float *w, int64_t T, int k, int n_shared, int H, int64_t R, void *out, int out_dtype) {
-  for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
-    for (int c = 8 * threadIdx.x; c < H; c += 8 * blockDim.x) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < k; ++s) {
-        const int32_t r = inv_perm[t * k + s];
-        if (r < 0 || r >= R) continue;  // never for a schedule from moeq_permute
-        const float wt = w[t * k + s];
-        float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < splits; ++sp) {
-          float v[8];
-          load_y8<YDT>(y, sp * split_stride + int64_t(r) * ldy + c, v);
+  const int ncb = (H + 511) / 512;
+  for (int64_t blk = blockIdx.x; blk < T * ncb; blk += gridDim.x) {
+    const int64_t t = blk / ncb;
+    const int c = int(blk % ncb) * 512 + 8 * threadIdx.x;
+    if (c >= H) continue;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int s = 0; s < k; ++s) {
+      const int32_t r = inv_perm[t * k + s];
+      if (r < 0 || r >= R) continue;  // never for a schedule from moeq_permute
+      const float wt = w[t * k + s];
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < splits; ++sp) {
+        float v[8];
+        load_y8<YDT>(y, sp * split_stride + int64_t(r) * ldy + c, v);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) sum[j] += v[j];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wt, sum[j], acc[j]);
+        for (int j = 0; j < 8; ++j) sum[j] += v[j];
       }
-      for (int v = 0; v < n_shared; ++v) {
-        const int64_t r = T * k + int64_t(v) * T + t;
-        for (int sp = 0; sp < splits; ++sp) {
-          float y8[8];
-          load_y8<YDT>(y, sp * split_stride + r * ldy + c, y8);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[j] += y8[j];
-        }
-      }
-      const int64_t o = t * H + c;
-      if (out_dtype == MOEQ_F32) {
-        float4 *p = reinterpret_cast<float4 *>(static_cast<float *>(out) + o);
-        p[0] = (float4){acc[0], acc[1], acc[2], acc[3]};
-        p[1] = (float4){acc[4], acc[5], acc[6], acc[7]};
-      } else {
-        uint32_t ws[4];
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wt, sum[j], acc[j]);
+    }
+    for (int v = 0; v < n_shared; ++v) {
+      const int64_t r = T * k + int64_t(v) * T + t;
+      for (int sp = 0; sp < splits; ++sp) {
+        float y8[8];
+        load_y8<YDT>(y, sp * split_stride + r * ldy + c, y8);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint16_t lo, hi;
-          if (out_dtype == MOEQ_BF16) {
-            lo = f32_to_bf16(acc[2 * j]);
-            hi = f32_to_bf16(acc[2 * j + 1]);
-          } else {
-            lo = f32_to_f16_bits(acc[2 * j]);
-            hi = f32_to_f16_bits(acc[2 * j + 1]);
-          }
-          ws[j] = uint32_t(lo) | (uint32_t(hi) << 16);
-        }
-        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o) = (uint4){ws[0], ws[1], ws[2], ws[3]};
+        for (int j = 0; j < 8; ++j) acc[j] += y8[j];
       }
+    }
+    const int64_t o = t * H + c;
+    if (out_dtype == MOEQ_F32) {
+      float4 *p = reinterpret_cast<float4 *>(static_cast<float *>(out) + o);
+      p[0] = (float4){acc[0], acc[1], acc[2], acc[3]};
+      p[1] = (float4){acc[4], acc[5], acc[6], acc[7]};
+    } else {
+      uint32_t ws[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint16_t lo, hi;
+        if (out_dtype == MOEQ_BF16) {
+          lo = f32_to_bf16(acc[2 * j]);
+          hi = f32_to_bf16(acc[2 * j + 1]);
+        } else {
+          lo = f32_to_f16_bits(acc[2 * j]);
+          hi = f32_to_f16_bits(acc[2 * j + 1]);
+        }
+        ws[j] = uint32_t(lo) | (uint32_t(hi) << 16);
+      }
+      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + o) = (uint4){ws[0], ws[1], ws[2], ws[3]};
     }
   }
 }
@@ -99,7 +104,8 @@ extern "C" int moeq_combine(const void *y, int y_dtype, int splits, int64_t spli
   if (splits > 1 && split_stride < (T * top_k + int64_t(n_shared) * T) * ldy)
     return fail(MOEQ_ERR_INVALID, "combine: split_stride=%lld too small", (long long)split_stride);
   const int64_t R = T * top_k + int64_t(n_shared) * T;
-  dim3 grid(unsigned(std::min<int64_t>(T, 65535))), block(256);
+  const int64_t blocks = T * ((H + 511) / 512);
+  dim3 grid(unsigned(std::min<int64_t>(blocks, 1 << 20))), block(64);
   hipStream_t s = as_stream(stream);
   if (y_dtype == MOEQ_F32)
     combine_kernel<MOEQ_F32><<<grid, block, 0, s>>>(y, splits, split_stride, ldy, inv_perm, w, T,

@@ -83,7 +83,7 @@ extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
 // driver sizes its launches with it.
 template <int BM>
 static int tile_n(bool silu) {
-  return silu ? Shape<BM, true>::NW * Shape<BM, true>::NB * 16 : Shape<BM, false>::NW * Shape<BM, false>::NB * 16;
+  return silu ? tile_cols<Shape<BM, true>, false>() : tile_cols<Shape<BM, false>, false>();
 }
 
 extern "C" int moeq_gemm_tile_n(int bm, int epilogue) {

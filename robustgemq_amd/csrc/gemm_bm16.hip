@@ -3,17 +3,27 @@
 
 namespace moeq {
 
+template <int ADT, int ODT, bool SILU>
+static int launch16(const GemmArgs &g, int max_tiles, int splits, hipStream_t s) {
+  // Few column blocks (small decode batches): split K over the waves of
+  // 16-column blocks instead, so enough waves keep weight fetches in flight.
+  using S = Shape<16, SILU>;
+  const int64_t col_blocks = int64_t(max_tiles) * cdiv(g.N, tile_cols<S, false>());
+  if (col_blocks < 512) return launch_one<16, SILU, ADT, ODT, true>(g, max_tiles, splits, s);
+  return launch_one<16, SILU, ADT, ODT, false>(g, max_tiles, splits, s);
+}
+
 template <>
 int launch_grouped_gemm<16>(const GemmArgs &g, bool silu, int a_dtype, int out_dtype, int max_tiles,
                             int splits, hipStream_t s) {
   const bool bf = a_dtype == MOEQ_BF16;
-  if (silu) return bf ? launch_one<16, true, MOEQ_BF16, MOEQ_F16>(g, max_tiles, splits, s)
-                      : launch_one<16, true, MOEQ_F16, MOEQ_F16>(g, max_tiles, splits, s);
+  if (silu) return bf ? launch16<MOEQ_BF16, MOEQ_F16, true>(g, max_tiles, splits, s)
+                      : launch16<MOEQ_F16, MOEQ_F16, true>(g, max_tiles, splits, s);
   if (out_dtype == MOEQ_F32)
-    return bf ? launch_one<16, false, MOEQ_BF16, MOEQ_F32>(g, max_tiles, splits, s)
-              : launch_one<16, false, MOEQ_F16, MOEQ_F32>(g, max_tiles, splits, s);
-  return bf ? launch_one<16, false, MOEQ_BF16, MOEQ_F16>(g, max_tiles, splits, s)
-            : launch_one<16, false, MOEQ_F16, MOEQ_F16>(g, max_tiles, splits, s);
+    return bf ? launch16<MOEQ_BF16, MOEQ_F32, false>(g, max_tiles, splits, s)
+              : launch16<MOEQ_F16, MOEQ_F32, false>(g, max_tiles, splits, s);
+  return bf ? launch16<MOEQ_BF16, MOEQ_F16, false>(g, max_tiles, splits, s)
+            : launch16<MOEQ_F16, MOEQ_F16, false>(g, max_tiles, splits, s);
 }
 
 }  // namespace moeq

@@ -24,6 +24,8 @@
 // template parameter chosen per tile.  Accumulation is fp32.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace moeq {
@@ -149,7 +151,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, int MBA>
+template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, int MBA, bool KS>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, int mcount, int nt,
                                           int c0, int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {
   constexpr int NT = NW * 64;
@@ -158,7 +160,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, kb = lane >> 4;
   const int N = g.N;
-  const int n_wave = nt * (NW * NB * 16) + wave * NB * 16;
+  // KS (16-row blocks of small launches): all waves share the block's
+  // columns and split K instead
+  const int n_wave = KS ? nt * (NB * 16) : nt * (NW * NB * 16) + wave * NB * 16;
 
   // Expert bases are wave-uniform; each lane adds 32-bit byte offsets (one
   // expert's words and scales stay far below 2 GiB).
@@ -216,8 +220,95 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
 
   const char *abytes = static_cast<const char *>(g.a);
 
-  if constexpr (BM == 16) {
-    // ---------------- decode shapes: A fragments straight from global memory
+  if constexpr (BM == 16 && KS) {
+    // ---------------- small decode launches (KS): the NW waves share the
+    // block's columns and take interleaved K chunks (wave w: chunks c0 + w,
+    // c0 + w + NW, ...); their partial sums meet in LDS afterwards.  A wave
+    // with at most 8 chunks fetches all of them at once, a longer one keeps
+    // a 4-chunk ring in flight.  Steps past a wave's last chunk re-read a
+    // valid chunk and multiply it by a zero A fragment, so every fetch and
+    // MFMA is unconditional (no joins for the wait counts to merge).
+    constexpr int AES = 2;
+    const int rr = row0 + min(l16, mcount - 1);
+    const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
+    const char *arow = abytes + src * g.lda * AES;
+    const int nc = c1 > c0 + wave ? (c1 - c0 - wave + NW - 1) / NW : 0;  // this wave's chunks
+    auto fetch = [&](int j, uint4 (&av)[4], uint32_t (&w)[NP][NB][BITS], uint32_t (&sz)[NP][NB]) {
+      const int c = c0 + wave + NW * min(j, max(nc - 1, 0));
+      const uint4 *pa = reinterpret_cast<const uint4 *>(arow + (int64_t(c) * 128 + 32 * kb) * AES);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[t] = pa[t];
+      load_b(c, w, sz);
+    };
+    auto step = [&](bool live, const uint4 (&av)[4], const uint32_t (&w)[NP][NB][BITS], const uint32_t (&sz)[NP][NB]) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const f16x8 A = live ? to_f16x8<ADT>(av[t]) : f16x8{};
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const f16x8 B = deq_frag<BITS, DQ>(w[p][nb], sz[p][nb], t);
+            acc[p][0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[p][0][nb], 0, 0, 0);
+          }
+      }
+    };
+    auto all_at_once = [&](auto slots) {
+      constexpr int S = decltype(slots)::value;
+      uint4 ar[S][4];
+      uint32_t wr[S][NP][NB][BITS], sr[S][NP][NB];
+#pragma unroll
+      for (int j = 0; j < S; ++j) fetch(j, ar[j], wr[j], sr[j]);
+#pragma unroll
+      for (int j = 0; j < S; ++j) step(j < nc, ar[j], wr[j], sr[j]);
+    };
+    if (nc == 1) {
+      all_at_once(std::integral_constant<int, 1>{});
+    } else if (nc == 2) {
+      all_at_once(std::integral_constant<int, 2>{});
+    } else if (nc > 2 && nc <= 4) {
+      all_at_once(std::integral_constant<int, 4>{});
+    } else if (nc > 4 && nc <= 8) {
+      all_at_once(std::integral_constant<int, 8>{});
+    } else if (nc > 8) {
+      constexpr int DEPTH = 4;
+      uint4 ar[DEPTH][4];
+      uint32_t wr[DEPTH][NP][NB][BITS], sr[DEPTH][NP][NB];
+#pragma unroll
+      for (int d = 0; d < DEPTH - 1; ++d) fetch(d, ar[d], wr[d], sr[d]);
+      for (int j0 = 0; j0 < nc; j0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+          const int nx = (d + DEPTH - 1) % DEPTH;
+          fetch(j0 + d + DEPTH - 1, ar[nx], wr[nx], sr[nx]);
+          step(j0 + d < nc, ar[d], wr[d], sr[d]);
+        }
+      }
+    }
+    // partial sums of the NW waves -> wave 0, added in wave order
+    float *red = reinterpret_cast<float *>(&As0[0][0]);
+    if (wave > 0) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) red[(((wave - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane] = acc[p][0][nb][i];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[p][0][nb][i] += red[(((w - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane];
+  } else if constexpr (BM == 16) {
+    // ---------------- decode launches with enough column blocks: each wave
+    // owns NB * 16 columns and runs the whole K range, A fragments straight
+    // from global memory, one chunk fetched ahead.
     constexpr int AES = 2;
     const int rr = row0 + min(l16, mcount - 1);
     const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
@@ -363,11 +454,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
   }
 }
 
-template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ>
+template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, bool KS>
 __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0, int mcount, int nt, int c0,
                                               int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {
   const int mb_act = (mcount + 15) >> 4;
-#define MOEQ_T(M) gemm_tile<BM, NW, NB, NP, EPI, ADT, ODT, BITS, DQ, M>(g, e, row0, mcount, nt, c0, c1, As0, As1)
+#define MOEQ_T(M) gemm_tile<BM, NW, NB, NP, EPI, ADT, ODT, BITS, DQ, M, KS>(g, e, row0, mcount, nt, c0, c1, As0, As1)
   if constexpr (BM == 16) {
     MOEQ_T(1);
   } else if constexpr (BM == 32) {
@@ -384,7 +475,7 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
 
 // Two work-groups per CU for the 32..128-row shapes and one 8-wave group for
 // the 256-row shape (its two A buffers take 128 KB of LDS): 2 waves per SIMD.
-template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT>
+template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, bool KS>
 __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
   // The grid is sized for the host-side bound on row tiles; blocks past the
   // real count (read from the device schedule) exit together.  Work-groups
@@ -398,7 +489,9 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
   const unsigned L = b < V8 ? (b & 7u) * (V8 >> 3) + (b >> 3) : b;
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
-  __shared__ uint4 As0[BM == 16 ? 1 : BM][16];
+  // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * NB * 4
+  // floats per lane, at most 12 KB
+  __shared__ uint4 As0[BM == 16 ? 48 : BM][16];
   __shared__ uint4 As1[BM == 16 ? 1 : BM][16];
   const int32_t *tp = g.tiles + 4 * mt;
   const int e = tp[0], row0 = tp[1], mcount = tp[2];
@@ -406,7 +499,7 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
   const int c1 = min(c0 + g.chunks_per_split, g.nchunks);
   const int bits = g.p[0].nbits[e];
   const int dq = g.dq_mode;
-#define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D>(g, e, row0, mcount, nt, c0, c1, As0, As1)
+#define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D, KS>(g, e, row0, mcount, nt, c0, c1, As0, As1)
 #define MOEQ_BITS(B)                                                   \
   if (dq == MOEQ_DQ_HQQ_INT) MOEQ_TILE(B, MOEQ_DQ_HQQ_INT);           \
   else if (dq == MOEQ_DQ_HQQ) MOEQ_TILE(B, MOEQ_DQ_HQQ);              \
@@ -422,9 +515,12 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
 }
 
 // Launch shapes: (NW waves, NB 16-column blocks per wave) for each BM and
-// epilogue.  Column tile width = NW * NB * 16.
+// epilogue.  Column tile width = NW * NB * 16, except for 16-row blocks whose
+// waves split K over the same NB * 16 columns.
 template <int BM, bool SILU>
 struct Shape;
+template <class S, bool KS>
+constexpr int tile_cols() { return KS ? S::NB * 16 : S::NW * S::NB * 16; }
 template <> struct Shape<16, true> { static constexpr int NW = 4, NB = 1; };
 template <> struct Shape<16, false> { static constexpr int NW = 4, NB = 2; };
 template <> struct Shape<32, true> { static constexpr int NW = 4, NB = 2; };
@@ -443,15 +539,16 @@ template <int BM>
 int launch_grouped_gemm(const GemmArgs &g, bool silu, int a_dtype, int out_dtype, int max_tiles, int splits,
                         hipStream_t s);
 
-template <int BM, bool SILU, int ADT, int ODT>
+template <int BM, bool SILU, int ADT, int ODT, bool KS = false>
 inline int launch_one(const GemmArgs &g0, int max_tiles, int splits, hipStream_t s) {
   using S = Shape<BM, SILU>;
+  static_assert(!KS || BM == 16, "K split over waves is a 16-row block variant");
   GemmArgs g = g0;
-  g.n_ntiles = int(cdiv(g.N, S::NW * S::NB * 16));
+  g.n_ntiles = int(cdiv(g.N, tile_cols<S, KS>()));
   const int64_t blocks = int64_t(max_tiles) * g.n_ntiles;
   if (blocks > 0x7fffffff) return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: grid too large");
   dim3 grid(unsigned(blocks), 1, unsigned(splits)), block(S::NW * 64);
-  grouped_gemm_kernel<BM, S::NW, S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ADT, ODT>
+  grouped_gemm_kernel<BM, S::NW, S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ADT, ODT, KS>
       <<<grid, block, 0, s>>>(g);
   return check_launch("grouped_gemm");
 }

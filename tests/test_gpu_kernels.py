@@ -186,6 +186,37 @@ def test_grouped_gemm_store_matches_fp32(device, bm, mode, g):
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("K", [384, 1024, 1536, 3072, 5120])
+def test_grouped_gemm_decode_k_split_depths(device, K):
+    """16-row launches with few column blocks split K over the waves: one,
+    two, up to four, up to eight chunks per wave fetched at once, and the
+    4-deep ring beyond that; rows of 1..16 tokens and a zero-row expert."""
+    from robustgemq_amd import ops
+    _say(f"[gemm/decode k-split] K={K}")
+    rng = np.random.default_rng(K)
+    E, N = 4, 96
+    bits = [2, 3, 4, 1]
+    proj, dense = _make_proj(device, rng, E, K, N, bits, 64, "int")
+    counts = [1, 16, 0, 5]
+    rows = sum(counts)
+    x = (rng.standard_normal((rows, K)) * 0.5).astype(np.float16)
+    tiles, r = [], 0
+    for e, m in enumerate(counts):
+        for j in range(0, m, 16):
+            tiles.append((e, r + j, min(16, m - j), 0))
+        r += m
+    tt = torch.tensor(tiles, dtype=torch.int32, device=device)
+    n = torch.tensor([len(tiles)], dtype=torch.int32, device=device)
+    out = ops.grouped_gemm(torch.from_numpy(x).to(device), rows, N, tt, n, len(tiles), 16, proj,
+                           out_dtype=torch.float32)
+    got = to_np(out)
+    r = 0
+    for e, m in enumerate(counts):
+        ref = x[r:r + m].astype(np.float32) @ dense[e]
+        np.testing.assert_allclose(got[r:r + m], ref, rtol=1e-4, atol=1e-4)
+        r += m
+
+
 @pytest.mark.parametrize("bm", [16, 128, 256])
 @pytest.mark.parametrize("adt", [torch.float16, torch.bfloat16])
 def test_grouped_gemm_silu_mul_and_splitk(device, bm, adt):
