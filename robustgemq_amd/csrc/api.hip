@@ -4,7 +4,7 @@
 
 #include <algorithm>
 
-#include "common.h"
+#include "routing.h"
 
 extern "C" int moeq_gemm_tile_n(int bm, int epilogue);
 
@@ -143,14 +143,29 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
   int32_t *tiles = static_cast<int32_t *>(at(p.off_tiles));
   int32_t *n_tiles = static_cast<int32_t *>(at(p.off_ntiles));
 
-  rc = moeq_route(x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
-                  m->top_k, m->norm_topk, logits_out, idx, w, at(p.off_route),
-                  moeq_route_workspace_size(T, m->n_experts), stream);
-  if (rc) return rc;
-  rc = moeq_permute(idx, T, m->top_k, m->n_experts, m->n_shared, p.bm, counts, offsets, row_token,
-                    row_pair, inv, tiles, n_tiles, at(p.off_perm),
-                    moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared), stream);
-  if (rc) return rc;
+  if (T <= 64 && m->hidden % 8 == 0 && m->hidden <= 4096 &&
+      topk_permute_fits(T, m->top_k, m->n_experts, m->n_shared)) {
+    // small batches: logits, then top-k and the permutation in one work-group
+    const int ldt = m->gate_dtype == MOEQ_F32 ? MOEQ_F32 : m->act_dtype;
+    void *lg = logits_out ? logits_out : at(p.off_route);
+    const int lg_dt = logits_out ? ldt : MOEQ_F32;
+    RouteArgs ra{x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
+                 m->top_k, m->norm_topk ? 1 : 0, lg, ldt, lg_dt, idx, w};
+    hipStream_t s = as_stream(stream);
+    if ((rc = launch_route_logits(ra, s))) return rc;
+    rc = launch_topk_permute(lg, lg_dt, T, m->n_experts, m->top_k, m->norm_topk ? 1 : 0, idx, w, m->n_shared,
+                             p.bm, counts, offsets, row_token, row_pair, inv, tiles, n_tiles, s);
+    if (rc) return rc;
+  } else {
+    rc = moeq_route(x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
+                    m->top_k, m->norm_topk, logits_out, idx, w, at(p.off_route),
+                    moeq_route_workspace_size(T, m->n_experts), stream);
+    if (rc) return rc;
+    rc = moeq_permute(idx, T, m->top_k, m->n_experts, m->n_shared, p.bm, counts, offsets, row_token,
+                      row_pair, inv, tiles, n_tiles, at(p.off_perm),
+                      moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared), stream);
+    if (rc) return rc;
+  }
 
   const void *xa = x;
   int xa_dtype = m->act_dtype;

@@ -13,7 +13,7 @@
 //               rows already emitted for that expert.
 #include <algorithm>
 
-#include "common.h"
+#include "routing.h"
 
 namespace moeq {
 
@@ -233,7 +233,7 @@ constexpr int kFusedWaves = 16;
 constexpr int kFusedPairs = kFusedWaves * 512;
 constexpr int kFusedExperts = 256;
 
-__global__ __launch_bounds__(1024) void permute_fused_kernel(
+__device__ void permute_block(
     const int32_t *idx, int64_t T, int k, int E, int n_shared, int bm, int max_tiles, int key_bits,
     int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *row_pair, int32_t *inv_perm,
     int32_t *tiles, int32_t *n_tiles) {
@@ -301,6 +301,68 @@ __global__ __launch_bounds__(1024) void permute_fused_kernel(
   }
 }
 
+__global__ __launch_bounds__(1024) void permute_fused_kernel(
+    const int32_t *idx, int64_t T, int k, int E, int n_shared, int bm, int max_tiles, int key_bits,
+    int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *row_pair, int32_t *inv_perm,
+    int32_t *tiles, int32_t *n_tiles) {
+  permute_block(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
+                inv_perm, tiles, n_tiles);
+}
+
+// Top-k of every token (wave t % 16 takes token t), then the permutation of
+// the selection by the same work-group: one launch instead of two for small
+// batches.  The selected indices are read back after the barrier, which
+// makes the waves' global stores visible to the whole work-group.
+template <int EREG>
+__global__ __launch_bounds__(1024) void topk_permute_kernel(
+    const void *logits, int dtype, int64_t T, int E, int k, int norm, int32_t *idx, float *w,
+    int n_shared, int bm, int max_tiles, int key_bits, int32_t *counts, int32_t *offsets,
+    int32_t *row_token, int32_t *row_pair, int32_t *inv_perm, int32_t *tiles, int32_t *n_tiles) {
+  const int lane = lane_id();
+  for (int64_t t = threadIdx.x >> 6; t < T; t += kFusedWaves) {
+    float vals[EREG];
+#pragma unroll
+    for (int r = 0; r < EREG; ++r) {
+      const int e = 64 * r + lane;
+      vals[r] = e < E ? load_as_f32(logits, dtype, t * E + e) : -INFINITY;
+    }
+    select_topk<EREG>(vals, E, k, norm, t, idx, w);
+  }
+  __syncthreads();
+  permute_block(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
+                inv_perm, tiles, n_tiles);
+}
+
+bool topk_permute_fits(int64_t T, int k, int E, int n_shared) {
+  return T * k <= kFusedPairs && E + n_shared <= kFusedExperts && k <= kMaxTopK;
+}
+
+static int key_bits_for(int E) {
+  int b = 1;
+  while ((1 << b) < E) ++b;
+  return b;
+}
+
+int launch_topk_permute(const void *logits, int dtype, int64_t T, int E, int k, int norm, int32_t *idx,
+                        float *w, int n_shared, int bm, int32_t *counts, int32_t *offsets,
+                        int32_t *row_token, int32_t *row_pair, int32_t *inv_perm, int32_t *tiles,
+                        int32_t *n_tiles, hipStream_t s) {
+  if (!topk_permute_fits(T, k, E, n_shared)) return fail(MOEQ_ERR_UNSUPPORTED, "topk_permute: batch too large");
+  const int max_tiles = moeq_max_tiles(T, k, E, n_shared, bm);
+  const int kb = key_bits_for(E);
+#define MOEQ_TP(R)                                                                                      \
+  topk_permute_kernel<R><<<1, 1024, 0, s>>>(logits, dtype, T, E, k, norm, idx, w, n_shared, bm, max_tiles, \
+                                            kb, counts, offsets, row_token, row_pair, inv_perm, tiles,   \
+                                            n_tiles)
+  switch (ereg_for(E)) {
+    case 1: MOEQ_TP(1); break;
+    case 2: MOEQ_TP(2); break;
+    default: MOEQ_TP(4); break;  // E <= kFusedExperts = 256
+  }
+#undef MOEQ_TP
+  return check_launch("route/topk_permute");
+}
+
 }  // namespace moeq
 
 using namespace moeq;
@@ -335,8 +397,7 @@ extern "C" int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
   size_t need = moeq_permute_workspace_size(T, top_k, E, n_shared);
   if (!ws || ws_bytes < need)
     return fail(MOEQ_ERR_WORKSPACE, "permute: workspace %zu < %zu bytes", ws_bytes, need);
-  int key_bits = 1;
-  while ((1 << key_bits) < E) ++key_bits;
+  const int key_bits = key_bits_for(E);
   hipStream_t s = as_stream(stream);
   const int max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm);
   if (T * top_k <= kFusedPairs && E + n_shared <= kFusedExperts) {

@@ -5,131 +5,9 @@
 // The xor butterfly (o = 32 .. 1, v <- v + v[l ^ o]) gives every lane the
 // same value because fp32 addition is commutative.  oracle/router_exact.c
 // replays exactly this order, so routing is bit-reproducible on the CPU.
-#include <float.h>
-
-#include "common.h"
+#include "routing.h"
 
 namespace moeq {
-
-constexpr int kMaxTopK = 16;
-
-struct RouteArgs {
-  const void *x;
-  int x_dtype;
-  int64_t T;
-  int H;
-  const void *wg;
-  int wg_dtype;
-  const float *bias;  // may be null
-  int E, k, norm;
-  void *logits;      // rounded logits [T, E]
-  int logits_dtype;  // rounding target of the logits
-  int store_dtype;   // element type of `logits` (logits_dtype, or F32 scratch)
-  int32_t *idx;
-  float *w;
-};
-
-__device__ __forceinline__ float round_logit(float v, int dtype) {
-  if (dtype == MOEQ_F16) return (float)(f16)v;
-  if (dtype == MOEQ_BF16) return bf16_to_f32(f32_to_bf16(v));
-  return v;
-}
-
-__device__ __forceinline__ void store_logit(void *p, int dtype, int64_t i, float v) {
-  if (dtype == MOEQ_F32)
-    static_cast<float *>(p)[i] = v;
-  else if (dtype == MOEQ_BF16)
-    static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
-  else
-    static_cast<uint16_t *>(p)[i] = f32_to_f16_bits(v);
-}
-
-// Loads 8 consecutive elements starting at element i and widens them to fp32.
-__device__ __forceinline__ void load8(const void *p, int dtype, int64_t i, float (&o)[8]) {
-  if (dtype == MOEQ_F32) {
-    const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
-    float4 a = q[0], b = q[1];
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-  } else {
-    uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
-    uint32_t ws[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint16_t lo = uint16_t(ws[j] & 0xffffu), hi = uint16_t(ws[j] >> 16);
-      if (dtype == MOEQ_BF16) {
-        o[2 * j] = bf16_to_f32(lo);
-        o[2 * j + 1] = bf16_to_f32(hi);
-      } else {
-        o[2 * j] = f16_bits_to_f32(lo);
-        o[2 * j + 1] = f16_bits_to_f32(hi);
-      }
-    }
-  }
-}
-
-// Top-k of the logits held by one wave (expert e = 64 r + lane in vals[r]),
-// ranked by value with ties to the lower index; softmax weights over all E
-// experts; optional renormalisation over the selected k.  Writes row t.
-template <int EREG>
-__device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
-                            int64_t t, int32_t *idx_out, float *w_out) {
-  const int lane = lane_id();
-  bool avail[EREG];
-#pragma unroll
-  for (int r = 0; r < EREG; ++r) {
-    int e = 64 * r + lane;
-    avail[r] = e < E;
-    if (!avail[r] || vals[r] != vals[r]) vals[r] = -INFINITY;  // NaN ranks last
-  }
-  int sel_i[kMaxTopK];
-  float sel_v[kMaxTopK];
-  for (int s = 0; s < k; ++s) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int r = 0; r < EREG; ++r) {
-      int e = 64 * r + lane;
-      if (avail[r] && (vals[r] > bv || (vals[r] == bv && e < bi))) {
-        bv = vals[r];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      float ov = __shfl_xor(bv, o);
-      int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    sel_i[s] = bi;
-    sel_v[s] = bv;
-#pragma unroll
-    for (int r = 0; r < EREG; ++r)
-      if (64 * r + lane == bi) avail[r] = false;
-  }
-  const float m = sel_v[0];
-  float den = 0.f;
-#pragma unroll
-  for (int r = 0; r < EREG; ++r)
-    if (64 * r + lane < E) den += __expf(vals[r] - m);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o);
-  float p[kMaxTopK];
-  float psum = 0.f;
-  for (int s = 0; s < k; ++s) {
-    p[s] = __expf(sel_v[s] - m) / den;
-    psum += p[s];
-  }
-  for (int s = 0; s < k; ++s) {
-    if (lane == s) {
-      idx_out[t * k + s] = sel_i[s];
-      w_out[t * k + s] = norm ? p[s] / psum : p[s];
-    }
-  }
-}
 
 // Logits of a TT-token x EE-expert tile per wave.  Lane l runs the TT*EE
 // fused multiply-add chains over its k set (k = 512 i + 8 l + j), then every
@@ -216,8 +94,6 @@ __global__ __launch_bounds__(256) void topk_from_logits_kernel(
   select_topk<EREG>(vals, E, k, norm, t, idx, w);
 }
 
-static int ereg_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
-
 template <int TT, int EE>
 static void launch_logits(const RouteArgs &a, int maxch, hipStream_t s) {
   const int n_et = int(cdiv(a.E, EE));
@@ -243,6 +119,18 @@ static int launch_topk(const void *logits, int dtype, int64_t T, int E, int k, i
   return check_launch("route/topk");
 }
 
+
+// Small batches take one logit per wave (T * E waves) so enough waves read
+// the router weights at once; larger ones share loads over 4 x 4 tiles.  The
+// summation order of a logit is the same for every tiling.
+int launch_route_logits(const RouteArgs &a, hipStream_t s) {
+  const int maxch = a.H <= 512 ? 1 : a.H <= 1024 ? 2 : a.H <= 2048 ? 4 : 8;
+  if (a.T <= 32)
+    launch_logits<1, 1>(a, maxch, s);
+  else
+    launch_logits<4, 4>(a, maxch, s);
+  return check_launch("route/logits");
+}
 
 static bool valid_dtype(int d) { return d == MOEQ_F16 || d == MOEQ_BF16 || d == MOEQ_F32; }
 
@@ -282,12 +170,7 @@ extern "C" int moeq_route(const void *x, int x_dtype, int64_t T, int H,
   RouteArgs a{x, x_dtype, T, H, gate_w, gate_dtype, logit_bias, E, top_k, norm_topk ? 1 : 0,
               lg, ldt, lg_dt, idx_out, w_out};
   hipStream_t s = as_stream(stream);
-  const int maxch = H <= 512 ? 1 : H <= 1024 ? 2 : H <= 2048 ? 4 : 8;
-  if (T <= 2)
-    launch_logits<1, 4>(a, maxch, s);
-  else
-    launch_logits<4, 4>(a, maxch, s);
-  int rc = check_launch("route/logits");
+  int rc = launch_route_logits(a, s);
   if (rc) return rc;
   // the selection reads the rounded logits (stored as ldt, or exactly as fp32)
   return launch_topk(lg, lg_dt, T, E, top_k, norm_topk ? 1 : 0, idx_out, w_out, s);

@@ -1,0 +1,146 @@
+// Router helpers shared by the logits / top-k kernels (route.hip) and the
+// single-work-group top-k + permute kernel (permute.hip).
+#pragma once
+
+#include <float.h>
+
+#include "common.h"
+
+namespace moeq {
+
+constexpr int kMaxTopK = 16;
+
+struct RouteArgs {
+  const void *x;
+  int x_dtype;
+  int64_t T;
+  int H;
+  const void *wg;
+  int wg_dtype;
+  const float *bias;  // may be null
+  int E, k, norm;
+  void *logits;      // rounded logits [T, E]
+  int logits_dtype;  // rounding target of the logits
+  int store_dtype;   // element type of `logits` (logits_dtype, or F32 scratch)
+  int32_t *idx;
+  float *w;
+};
+
+__device__ __forceinline__ float round_logit(float v, int dtype) {
+  if (dtype == MOEQ_F16) return (float)(f16)v;
+  if (dtype == MOEQ_BF16) return bf16_to_f32(f32_to_bf16(v));
+  return v;
+}
+
+__device__ __forceinline__ void store_logit(void *p, int dtype, int64_t i, float v) {
+  if (dtype == MOEQ_F32)
+    static_cast<float *>(p)[i] = v;
+  else if (dtype == MOEQ_BF16)
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
+  else
+    static_cast<uint16_t *>(p)[i] = f32_to_f16_bits(v);
+}
+
+// Loads 8 consecutive elements starting at element i and widens them to fp32.
+__device__ __forceinline__ void load8(const void *p, int dtype, int64_t i, float (&o)[8]) {
+  if (dtype == MOEQ_F32) {
+    const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+    float4 a = q[0], b = q[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+    uint32_t ws[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint16_t lo = uint16_t(ws[j] & 0xffffu), hi = uint16_t(ws[j] >> 16);
+      if (dtype == MOEQ_BF16) {
+        o[2 * j] = bf16_to_f32(lo);
+        o[2 * j + 1] = bf16_to_f32(hi);
+      } else {
+        o[2 * j] = f16_bits_to_f32(lo);
+        o[2 * j + 1] = f16_bits_to_f32(hi);
+      }
+    }
+  }
+}
+
+// Top-k of the logits held by one wave (expert e = 64 r + lane in vals[r]),
+// ranked by value with ties to the lower index; softmax weights over all E
+// experts; optional renormalisation over the selected k.  Writes row t.
+template <int EREG>
+__device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
+                            int64_t t, int32_t *idx_out, float *w_out) {
+  const int lane = lane_id();
+  bool avail[EREG];
+#pragma unroll
+  for (int r = 0; r < EREG; ++r) {
+    int e = 64 * r + lane;
+    avail[r] = e < E;
+    if (!avail[r] || vals[r] != vals[r]) vals[r] = -INFINITY;  // NaN ranks last
+  }
+  int sel_i[kMaxTopK];
+  float sel_v[kMaxTopK];
+  for (int s = 0; s < k; ++s) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < EREG; ++r) {
+      int e = 64 * r + lane;
+      if (avail[r] && (vals[r] > bv || (vals[r] == bv && e < bi))) {
+        bv = vals[r];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      float ov = __shfl_xor(bv, o);
+      int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    sel_i[s] = bi;
+    sel_v[s] = bv;
+#pragma unroll
+    for (int r = 0; r < EREG; ++r)
+      if (64 * r + lane == bi) avail[r] = false;
+  }
+  const float m = sel_v[0];
+  float den = 0.f;
+#pragma unroll
+  for (int r = 0; r < EREG; ++r)
+    if (64 * r + lane < E) den += __expf(vals[r] - m);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o);
+  float p[kMaxTopK];
+  float psum = 0.f;
+  for (int s = 0; s < k; ++s) {
+    p[s] = __expf(sel_v[s] - m) / den;
+    psum += p[s];
+  }
+  for (int s = 0; s < k; ++s) {
+    if (lane == s) {
+      idx_out[t * k + s] = sel_i[s];
+      w_out[t * k + s] = norm ? p[s] / psum : p[s];
+    }
+  }
+}
+
+static inline int ereg_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
+
+// Logits of every (token, expert) pair (rounded as RouteArgs asks), without
+// the selection; defined in route.hip.
+int launch_route_logits(const RouteArgs &a, hipStream_t s);
+
+// Top-k of T rows of logits followed by the token -> expert permutation, in
+// one work-group; valid when T * k <= kFusedPairs and E + n_shared <=
+// kFusedExperts (permute.hip).
+int launch_topk_permute(const void *logits, int dtype, int64_t T, int E, int k, int norm, int32_t *idx,
+                        float *w, int n_shared, int bm, int32_t *counts, int32_t *offsets,
+                        int32_t *row_token, int32_t *row_pair, int32_t *inv_perm, int32_t *tiles,
+                        int32_t *n_tiles, hipStream_t s);
+bool topk_permute_fits(int64_t T, int k, int E, int n_shared);
+
+}  // namespace moeq
