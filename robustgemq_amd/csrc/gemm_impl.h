@@ -220,21 +220,24 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
 
   const char *abytes = static_cast<const char *>(g.a);
 
-  if constexpr (BM == 16 && KS) {
-    // ---------------- small decode launches (KS): the NW waves share the
-    // block's columns and take interleaved K chunks (wave w: chunks c0 + w,
-    // c0 + w + NW, ...); their partial sums meet in LDS afterwards.  A wave
-    // with at most 8 chunks fetches all of them at once, a longer one keeps
-    // a 4-chunk ring in flight.  Steps past a wave's last chunk re-read a
-    // valid chunk and multiply it by a zero A fragment, so every fetch and
-    // MFMA is unconditional (no joins for the wait counts to merge).
+  if constexpr (BM == 16) {
+    // ---------------- decode shapes: A fragments straight from global memory.
+    // KS (small launches): the NW waves share the block's columns and take
+    // interleaved K chunks (wave w: chunks c0 + w, c0 + w + NW, ...), their
+    // partial sums meeting in LDS afterwards; otherwise each wave owns NB * 16
+    // columns and runs all chunks.  A wave with at most 8 chunks fetches all
+    // of them at once, a longer one keeps a 4-chunk ring in flight.  Steps
+    // past a wave's last chunk re-read a valid chunk and multiply it by a
+    // zero A fragment, so every fetch and MFMA is unconditional (no joins for
+    // the wait counts to merge).
     constexpr int AES = 2;
     const int rr = row0 + min(l16, mcount - 1);
     const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
     const char *arow = abytes + src * g.lda * AES;
-    const int nc = c1 > c0 + wave ? (c1 - c0 - wave + NW - 1) / NW : 0;  // this wave's chunks
+    const int cfirst = KS ? c0 + wave : c0, cstep = KS ? NW : 1;
+    const int nc = KS ? (c1 > c0 + wave ? (c1 - c0 - wave + NW - 1) / NW : 0) : max(c1 - c0, 0);
     auto fetch = [&](int j, uint4 (&av)[4], uint32_t (&w)[NP][NB][BITS], uint32_t (&sz)[NP][NB]) {
-      const int c = c0 + wave + NW * min(j, max(nc - 1, 0));
+      const int c = cfirst + cstep * min(j, max(nc - 1, 0));
       const uint4 *pa = reinterpret_cast<const uint4 *>(arow + (int64_t(c) * 128 + 32 * kb) * AES);
 #pragma unroll
       for (int t = 0; t < 4; ++t) av[t] = pa[t];
@@ -285,65 +288,27 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
         }
       }
     }
-    // partial sums of the NW waves -> wave 0, added in wave order
-    float *red = reinterpret_cast<float *>(&As0[0][0]);
-    if (wave > 0) {
-#pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) red[(((wave - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane] = acc[p][0][nb][i];
-    }
-    __syncthreads();
-    if (wave > 0) return;
-#pragma unroll
-    for (int w = 1; w < NW; ++w)
-#pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[p][0][nb][i] += red[(((w - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane];
-  } else if constexpr (BM == 16) {
-    // ---------------- decode launches with enough column blocks: each wave
-    // owns NB * 16 columns and runs the whole K range, A fragments straight
-    // from global memory, one chunk fetched ahead.
-    constexpr int AES = 2;
-    const int rr = row0 + min(l16, mcount - 1);
-    const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
-    const char *arow = abytes + src * g.lda * AES;
-    uint4 acur[4], anxt[4];
-    auto load_a = [&](int c, uint4 (&av)[4]) {
-      const uint4 *p = reinterpret_cast<const uint4 *>(arow + (int64_t(c) * 128 + 32 * kb) * AES);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) av[t] = p[t];
-    };
-    if (c0 < c1) {
-      load_a(c0, acur);
-      load_b(c0, wcur, scur);
-    }
-    for (int c = c0; c < c1; ++c) {
-      // The next chunk is fetched unconditionally (the last chunk re-reads
-      // itself): a conditional fetch joins two paths, and the wait counts
-      // merged at the join would then wait for the fetch just issued.
-      const int cn = min(c + 1, c1 - 1);
-      load_a(cn, anxt);
-      load_b(cn, wnxt, snxt);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const f16x8 A = to_f16x8<ADT>(acur[t]);
+    // KS: partial sums of the NW waves -> wave 0, added in wave order
+    if constexpr (KS) {
+      float *red = reinterpret_cast<float *>(&As0[0][0]);
+      if (wave > 0) {
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            const f16x8 B = deq_frag<BITS, DQ>(wcur[p][nb], scur[p][nb], t);
-            acc[p][0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[p][0][nb], 0, 0, 0);
-          }
-      }
+          for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acur[t] = anxt[t];
-      advance();
+            for (int i = 0; i < 4; ++i) red[(((wave - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane] = acc[p][0][nb][i];
+      }
+      __syncthreads();
+      if (wave > 0) return;
+#pragma unroll
+      for (int w = 1; w < NW; ++w)
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[p][0][nb][i] += red[(((w - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane];
     }
   } else {
     // ---------------- prefill shapes: A copied global -> LDS, double buffered

@@ -9,73 +9,10 @@
 
 namespace moeq {
 
-// Logits of a TT-token x EE-expert tile per wave.  Lane l runs the TT*EE
-// fused multiply-add chains over its k set (k = 512 i + 8 l + j), then every
-// chain is reduced with the xor butterfly; the order per logit is exactly the
-// one documented at the top of this file whatever the tiling.
 template <int TT, int EE, int MAXCH>
 __global__ __launch_bounds__(256) void logits_kernel(RouteArgs a, int n_et) {
-  const int lane = lane_id();
   const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t tt_tile = wave / n_et;
-  const int e0 = int(wave % n_et) * EE;
-  const int64_t t0 = tt_tile * TT;
-  if (t0 >= a.T) return;
-  float ch[TT][EE];
-#pragma unroll
-  for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-    for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = 0.f;
-#pragma unroll
-  for (int i = 0; i < MAXCH; ++i) {
-    const int k0 = 512 * i + 8 * lane;
-    if (k0 < a.H) {
-      float xv[TT][8], wv[EE][8];
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        if (t0 + tt < a.T) {
-          load8(a.x, a.x_dtype, (t0 + tt) * a.H + k0, xv[tt]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) xv[tt][j] = 0.f;
-        }
-      }
-#pragma unroll
-      for (int ee = 0; ee < EE; ++ee) {
-        if (e0 + ee < a.E) {
-          load8(a.wg, a.wg_dtype, int64_t(e0 + ee) * a.H + k0, wv[ee]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) wv[ee][j] = 0.f;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-          for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = __builtin_fmaf(xv[tt][j], wv[ee][j], ch[tt][ee]);
-    }
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-      for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = ch[tt][ee] + __shfl_xor(ch[tt][ee], o);
-  // every lane now holds all TT*EE logits; lane j stores logit j
-#pragma unroll
-  for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-    for (int ee = 0; ee < EE; ++ee) {
-      const int64_t t = t0 + tt;
-      const int e = e0 + ee;
-      if (lane == tt * EE + ee && t < a.T && e < a.E) {
-        float v = ch[tt][ee];
-        if (a.bias) v = v + a.bias[e];
-        store_logit(a.logits, a.store_dtype, t * a.E + e, round_logit(v, a.logits_dtype));
-      }
-    }
+  logit_tile<TT, EE, MAXCH>(a, (wave / n_et) * TT, int(wave % n_et) * EE);
 }
 
 template <int EREG>
