@@ -65,7 +65,8 @@ static Plan make_plan(const moeq_moe *m, int64_t T) {
   p.off_perm = take(moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared));
   p.off_route = take(moeq_route_workspace_size(T, m->n_experts));
   // the LDS-staged GEMM tiles (bm >= 32) read F16 rows
-  p.off_x16 = take(m->act_dtype == MOEQ_BF16 && p.bm >= 32 ? size_t(T) * m->hidden * 2 : 0);
+  // the expert GEMMs read F16 activations
+  p.off_x16 = take(m->act_dtype == MOEQ_BF16 ? size_t(T) * m->hidden * 2 : 0);
   p.off_h = take(size_t(p.rows) * m->inter * 2);
   p.off_y = take(size_t(p.splits) * p.rows * m->hidden * (p.y_dtype == MOEQ_F32 ? 4 : 2));
   p.total = o;
@@ -143,6 +144,7 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
   int32_t *tiles = static_cast<int32_t *>(at(p.off_tiles));
   int32_t *n_tiles = static_cast<int32_t *>(at(p.off_ntiles));
 
+  bool x16_done = false;
   if (T <= 64 && m->hidden % 8 == 0 && m->hidden <= 4096 &&
       topk_permute_fits(T, m->top_k, m->n_experts, m->n_shared)) {
     // small batches: logits, then top-k and the permutation in one work-group
@@ -150,7 +152,9 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
     void *lg = logits_out ? logits_out : at(p.off_route);
     const int lg_dt = logits_out ? ldt : MOEQ_F32;
     RouteArgs ra{x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
-                 m->top_k, m->norm_topk ? 1 : 0, lg, ldt, lg_dt, idx, w};
+                 m->top_k, m->norm_topk ? 1 : 0, lg, ldt, lg_dt, idx, w,
+                 m->act_dtype == MOEQ_BF16 ? static_cast<uint16_t *>(at(p.off_x16)) : nullptr};
+    x16_done = m->act_dtype == MOEQ_BF16;
     hipStream_t s = as_stream(stream);
     if ((rc = launch_route_logits(ra, s))) return rc;
     rc = launch_topk_permute(lg, lg_dt, T, m->n_experts, m->top_k, m->norm_topk ? 1 : 0, idx, w, m->n_shared,
@@ -169,11 +173,13 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
 
   const void *xa = x;
   int xa_dtype = m->act_dtype;
-  if (m->act_dtype == MOEQ_BF16 && p.bm >= 32) {
-    const int64_t n = T * m->hidden;
-    bf16_to_f16_kernel<<<dim3(unsigned(cdiv(n / 8, 256))), dim3(256), 0, as_stream(stream)>>>(
-        static_cast<const uint16_t *>(x), n, static_cast<uint16_t *>(at(p.off_x16)));
-    if ((rc = check_launch("moe/bf16_to_f16"))) return rc;
+  if (m->act_dtype == MOEQ_BF16) {
+    if (!x16_done) {
+      const int64_t n = T * m->hidden;
+      bf16_to_f16_kernel<<<dim3(unsigned(cdiv(n / 8, 256))), dim3(256), 0, as_stream(stream)>>>(
+          static_cast<const uint16_t *>(x), n, static_cast<uint16_t *>(at(p.off_x16)));
+      if ((rc = check_launch("moe/bf16_to_f16"))) return rc;
+    }
     xa = at(p.off_x16);
     xa_dtype = MOEQ_F16;
   }

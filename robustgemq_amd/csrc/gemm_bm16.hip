@@ -5,11 +5,13 @@ namespace moeq {
 
 template <int ADT, int ODT, bool SILU>
 static int launch16(const GemmArgs &g, int max_tiles, int splits, hipStream_t s) {
-  // Few column blocks (small decode batches): split K over the waves of
-  // 16-column blocks instead, so enough waves keep weight fetches in flight.
+  // Few column blocks (small decode batches) or a long K range: split K over
+  // the waves of 16-column blocks instead, so enough waves keep weight
+  // fetches in flight and no wave walks a long chain of chunks.
   using S = Shape<16, SILU>;
   const int64_t col_blocks = int64_t(max_tiles) * cdiv(g.N, tile_cols<S, false>());
-  if (col_blocks < 512) return launch_one<16, SILU, ADT, ODT, true>(g, max_tiles, splits, s);
+  const int chunks = int(cdiv(g.nchunks, splits));
+  if (col_blocks < 512 || chunks > 32) return launch_one<16, SILU, ADT, ODT, true>(g, max_tiles, splits, s);
   return launch_one<16, SILU, ADT, ODT, false>(g, max_tiles, splits, s);
 }
 

@@ -57,12 +57,12 @@ static int launch_topk(const void *logits, int dtype, int64_t T, int E, int k, i
 }
 
 
-// Small batches take one logit per wave (T * E waves) so enough waves read
-// the router weights at once; larger ones share loads over 4 x 4 tiles.  The
-// summation order of a logit is the same for every tiling.
+// Small batches take one logit per wave (up to 16384 waves) so enough waves
+// read the router weights at once; larger ones share loads over 4 x 4 tiles.
+// The summation order of a logit is the same for every tiling.
 int launch_route_logits(const RouteArgs &a, hipStream_t s) {
   const int maxch = a.H <= 512 ? 1 : a.H <= 1024 ? 2 : a.H <= 2048 ? 4 : 8;
-  if (a.T <= 32)
+  if (a.T * a.E <= 16384)
     launch_logits<1, 1>(a, maxch, s);
   else
     launch_logits<4, 4>(a, maxch, s);

@@ -24,6 +24,7 @@ struct RouteArgs {
   int store_dtype;   // element type of `logits` (logits_dtype, or F32 scratch)
   int32_t *idx;
   float *w;
+  uint16_t *x16 = nullptr;  // optional [T, H] fp16 copy of x, written by the expert-0 waves
 };
 
 __device__ __forceinline__ float round_logit(float v, int dtype) {
@@ -150,6 +151,13 @@ __device__ void logit_tile(const RouteArgs &a, int64_t t0, int e0) {
       for (int tt = 0; tt < TT; ++tt) {
         if (t0 + tt < a.T) {
           load8(a.x, a.x_dtype, (t0 + tt) * a.H + k0, xv[tt]);
+          if (a.x16 && e0 == 0) {  // the activations the expert GEMMs read, converted once
+            uint32_t h[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              h[j] = uint32_t(f32_to_f16_bits(xv[tt][2 * j])) | (uint32_t(f32_to_f16_bits(xv[tt][2 * j + 1])) << 16);
+            *reinterpret_cast<uint4 *>(a.x16 + (t0 + tt) * a.H + k0) = (uint4){h[0], h[1], h[2], h[3]};
+          }
         } else {
 #pragma unroll
           for (int j = 0; j < 8; ++j) xv[tt][j] = 0.f;
