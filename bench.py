@@ -5,14 +5,17 @@ Workload (configs[1] of BASELINE.json): OLMoE-1B-7B-shaped layer, hidden 2048,
 (50/25/25) group-64 HQQ weights, fp16 activations, synthetic data.  A step is
 one full layer forward (route, permute, grouped gate/up + SiLU*mul, grouped
 down, combine) over a 2048-token prefill batch already resident in HBM;
-`value` is prefill tokens/s.  The same run also reports prefill at 512 tokens
-and decode at batch 1 / 8 / 32 (graph-replayed, as the reference times decode
-under CUDA graphs), the live roofline of the dominant kernel (the grouped
-gate/up GEMM, MFMA-bound at this size), and the CPU baseline: the oracle's
-fp32 dequantize-then-matmul expert loop on a bounded token sample.
+`value` is prefill tokens/s.  The same run also reports prefill at 512 tokens,
+decode at batch 1 / 8 / 32 of this layer and at batch 1 / 16 / 64 of the
+Mixtral-shaped layer of configs[4] (HBM-bound; graph-replayed, as the
+reference times decode under CUDA graphs), the live roofline of the dominant
+kernel (the grouped gate/up GEMM, MFMA-bound at this size) with its HBM
+traffic from the committed rocprofv3 counter summary, and the CPU baseline:
+the oracle's fp32 dequantize-then-matmul expert loop on a bounded token
+sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
-                       [--tokens T] [--no-cpu] [--no-decode]
+                       [--tokens T] [--no-cpu] [--no-decode] [--no-mixtral]
 """
 
 import argparse
@@ -38,6 +41,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-mixtral", action="store_true", help="skip the Mixtral-shaped decode lines")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 256 MiB device-to-device copy first (reference size for HBM counters)")
@@ -150,10 +154,13 @@ def main():
     dn_flops = 2.0 * rows * cfg.hidden * cfg.inter
     gu_tflops = gu_flops / (kt["gate_up"] * 1e-3) / 1e12
     w_bytes_gu = layer.w1.weight_bytes(hit) + layer.w3.weight_bytes(hit)
+    kname = "grouped_gemm_kernel<BM=%d> gate/up (SiLU*mul epilogue)" % bm
+    traffic, tsrc = profile_traffic(kname, f"{cfg.name} T={T}")
     roofline = {"bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(gu_tflops / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
-                "kernel": "grouped_gemm_kernel<BM=%d> gate/up (SiLU*mul epilogue)" % bm,
-                "flops_per_launch": gu_flops, "avg_launch_ms": round(kt["gate_up"], 4)}
+                "frac": round(gu_tflops / PEAK_MFMA_F16_TFLOPS, 4), "traffic": traffic,
+                "kernel": kname, "flops_per_launch": gu_flops, "avg_launch_ms": round(kt["gate_up"], 4),
+                "algorithmic_bytes_per_launch": w_bytes_gu + rows * cfg.hidden * 2 + rows * cfg.inter * 2,
+                "traffic_source": tsrc}
     layer_flops = flops(cfg, T)
     extra = {
         "stage_ms": {k: round(v, 4) for k, v in kt.items()},
@@ -169,33 +176,17 @@ def main():
         ms = time_events(lambda: layer.forward(xp, want_logits=False), args.steps, args.warmup, stream)
         runs[f"prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4)}
     if not args.no_decode:
-        for B in cfg.runs.get("decode", ()):
-            xb = make_inputs(cfg, B, seed=2).to(dev)
-            ob = torch.empty((B, cfg.hidden), dtype=cfg.act_dtype, device=dev)
-            layer.forward(xb, out=ob, want_logits=False)  # sizes the workspace before capture
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            s = torch.cuda.Stream(dev)
-            s.wait_stream(stream)
-            with torch.cuda.stream(s):
-                layer.forward(xb, out=ob, want_logits=False)
-                torch.cuda.synchronize()
-                with torch.cuda.graph(g, stream=s):
-                    layer.forward(xb, out=ob, want_logits=False)
-            stream.wait_stream(s)
-            ref = ob.clone()
-            ms_graph = time_events(g.replay, args.steps * 5, args.warmup, stream)
-            assert torch.equal(ob, ref), "graph replay changed the decode output"
-            ms_eager = time_events(lambda: layer.forward(xb, out=ob, want_logits=False), args.steps, args.warmup,
-                                   stream)
-            idx_b = ops.route(xb, layer.gate_w, layer.top_k, layer.norm_topk, logits=False)[1]
-            hit_b = sorted(set(idx_b.cpu().numpy().reshape(-1).tolist()))
-            bytes_b = (layer.w1.weight_bytes(hit_b) + layer.w3.weight_bytes(hit_b) + layer.w2.weight_bytes(hit_b)
-                       + cfg.n_experts * cfg.hidden * 2 + 2 * B * cfg.hidden * 2)
-            runs[f"decode_B{B}"] = {"tokens_per_s": round(B / (ms_graph * 1e-3), 1), "ms_graph": round(ms_graph, 4),
-                                    "ms_eager": round(ms_eager, 4), "hit_experts": len(hit_b),
-                                    "alg_bytes": bytes_b,
-                                    "hbm_frac_layer": round(bytes_b / (ms_graph * 1e-3) / (PEAK_HBM_GBS * 1e9), 4)}
+        runs.update(decode_runs(cfg, layer, cfg.runs.get("decode", ()), args, stream, ""))
+    if not args.no_mixtral and args.config != "mixtral_mixed":
+        # the HBM-bound decode (two 55-100 MB experts per token)
+        mcfg = CONFIGS["mixtral_mixed"]
+        log("[bench] building mixtral_mixed (synthetic weights, seed 0) for decode")
+        mw = make_weights(mcfg, seed=0, quant_device=dev)
+        mlayer = build_block(mcfg, mw, device=dev)._layer
+        del mw
+        runs.update(decode_runs(mcfg, mlayer, mcfg.runs.get("decode", ()), args, stream, "mixtral_"))
+        del mlayer
+        torch.cuda.empty_cache()
     extra["runs"] = runs
 
     # ---------------- CPU baseline: oracle fp32 expert loop, bounded sample
@@ -214,6 +205,63 @@ def main():
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(line))
+
+
+def decode_runs(cfg, layer, batches, args, stream, tag):
+    """Decode steps (one layer forward of B tokens) replayed from a CUDA graph,
+    as the reference times decode under CUDA graphs; each replay's output is
+    checked against the eager one.  HBM fraction = algorithmic bytes (packed
+    codes + scale/zero of the hit experts, router, activations) / time / 8 TB/s."""
+    import torch
+
+    from robustgemq_amd import ops
+    from robustgemq_amd.synthetic import make_inputs
+    dev = torch.device("cuda:0")
+    out = {}
+    for B in batches:
+        xb = make_inputs(cfg, B, seed=2).to(dev)
+        ob = torch.empty((B, cfg.hidden), dtype=cfg.act_dtype, device=dev)
+        layer.forward(xb, out=ob, want_logits=False)  # sizes the workspace before capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(stream)
+        with torch.cuda.stream(s):
+            layer.forward(xb, out=ob, want_logits=False)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                layer.forward(xb, out=ob, want_logits=False)
+        stream.wait_stream(s)
+        ref = ob.clone()
+        ms_graph = time_events(g.replay, args.steps * 5, args.warmup, stream)
+        assert torch.equal(ob, ref), "graph replay changed the decode output"
+        ms_eager = time_events(lambda: layer.forward(xb, out=ob, want_logits=False), args.steps, args.warmup,
+                               stream)
+        idx_b = ops.route(xb, layer.gate_w, layer.top_k, layer.norm_topk, logits=False,
+                          logit_bias=layer.logit_bias)[1]
+        hit_b = sorted(set(idx_b.cpu().numpy().reshape(-1).tolist()))
+        bytes_b = (layer.w1.weight_bytes(hit_b) + layer.w3.weight_bytes(hit_b) + layer.w2.weight_bytes(hit_b)
+                   + cfg.n_experts * cfg.hidden * 2 + 2 * B * cfg.hidden * 2)
+        out[f"{tag}decode_B{B}"] = {"tokens_per_s": round(B / (ms_graph * 1e-3), 1), "ms_graph": round(ms_graph, 4),
+                                     "ms_eager": round(ms_eager, 4), "hit_experts": len(hit_b),
+                                     "alg_bytes": bytes_b,
+                                     "hbm_frac_layer": round(bytes_b / (ms_graph * 1e-3) / (PEAK_HBM_GBS * 1e9), 4)}
+    return out
+
+
+def profile_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the factors a
+    256 MiB copy calibrates), or None when no summary for them is committed."""
+    import re
+    path = os.path.join(ROOT, "profiles", "grouped_gemm_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        m = re.match(r"\|\s*`([^`]+)`\s*\|\s*`([^`]+)`\s*\|.*\|\s*(\d+)\s*\|\s*$", line)
+        if m and m.group(1) == kernel and m.group(2) == workload:
+            return int(m.group(3)), "profiles/grouped_gemm_hbm_traffic.md"
+    return None, None
 
 
 def cpu_baseline(cfg, w, budget_s):

@@ -138,8 +138,7 @@ int moeq_route_from_logits(const void *logits, int dtype, int64_t T, int E,
  *   inv_perm[T*top_k]                row of each (t, slot) pair,
  *   tiles[max_tiles*4]               (expert, row_start, row_count, 0): each
  *                                    expert's rows as full `bm`-row tiles
- *                                    plus one remainder tile; all full
- *                                    tiles first, then the remainders,
+ *                                    plus one remainder tile, in expert order,
  *   n_tiles[1].
  * max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm).
  * Replaces the one_hot / nonzero / torch.where grouping and its host syncs,

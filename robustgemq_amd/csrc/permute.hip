@@ -92,12 +92,12 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
                         int32_t *n_tiles, int *sh, int *s_off) {
   const int e = threadIdx.x, Et = E + n_shared;
   const int m = e < Et ? c : 0;
-  const int nfull = m / bm, npart = m % bm ? 1 : 0;
-  int tot_rows, tot_full, tot_part;
+  // an expert's full tiles, then its remainder tile; experts in order, so
+  // the tiles sharing an expert's weights are dispatched together
+  const int nt = (m + bm - 1) / bm;
+  int tot_rows, tot_tiles;
   const int off = block_exclusive_scan(m, sh, &tot_rows);
-  const int tb = block_exclusive_scan(nfull, sh, &tot_full);
-  const int tp0 = tot_full + block_exclusive_scan(npart, sh, &tot_part);
-  const int tot_tiles = tot_full + tot_part;
+  const int tb = block_exclusive_scan(nt, sh, &tot_tiles);
   if (e < Et) {
     counts[e] = c;
     offsets[e] = off;
@@ -109,21 +109,11 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
     // a corrupted idx from writing past the schedule buffer
     *n_tiles = min(tot_tiles, max_tiles);
   }
-  // Every expert's full tiles come first and the remainder tiles last: the
-  // GEMM work-groups are dispatched in tile order, so the long tiles start
-  // first and the short ones fill the tail of the launch.
-  for (int j = 0; j < nfull && tb + j < max_tiles; ++j) {
+  for (int j = 0; j < nt && tb + j < max_tiles; ++j) {
     int32_t *tp = tiles + 4 * (tb + j);
     tp[0] = e;
     tp[1] = off + j * bm;
-    tp[2] = bm;
-    tp[3] = 0;
-  }
-  if (npart && tp0 < max_tiles) {
-    int32_t *tp = tiles + 4 * tp0;
-    tp[0] = e;
-    tp[1] = off + nfull * bm;
-    tp[2] = m - nfull * bm;
+    tp[2] = min(bm, m - j * bm);
     tp[3] = 0;
   }
   __syncthreads();
