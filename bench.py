@@ -41,7 +41,8 @@ def parse():
     ap.add_argument("--tokens", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-mixtral", action="store_true", help="skip the Mixtral-shaped decode lines")
+    ap.add_argument("--no-mixtral", action="store_true", help="skip the Mixtral-shaped decode and stack lines")
+    ap.add_argument("--no-others", action="store_true", help="skip the Qwen3 and DeepSeek prefill lines")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 256 MiB device-to-device copy first (reference size for HBM counters)")
@@ -178,15 +179,36 @@ def main():
     if not args.no_decode:
         runs.update(decode_runs(cfg, layer, cfg.runs.get("decode", ()), args, stream, ""))
     if not args.no_mixtral and args.config != "mixtral_mixed":
-        # the HBM-bound decode (two 55-100 MB experts per token)
+        # the HBM-bound decode (two 55-100 MB experts per token) and
+        # the 16-layer stack at 1024-token prefill
         mcfg = CONFIGS["mixtral_mixed"]
-        log("[bench] building mixtral_mixed (synthetic weights, seed 0) for decode")
+        log("[bench] building mixtral_mixed (synthetic weights, seed 0)")
         mw = make_weights(mcfg, seed=0, quant_device=dev)
         mlayer = build_block(mcfg, mw, device=dev)._layer
         del mw
         runs.update(decode_runs(mcfg, mlayer, mcfg.runs.get("decode", ()), args, stream, "mixtral_"))
+        runs.update(stack_run(mcfg, mlayer, 16, 1024, args, stream))
         del mlayer
         torch.cuda.empty_cache()
+    if not args.no_others:
+        # configs[2] and configs[3] at their prefill sizes
+        for name in ("qwen3_mixed", "deepseek_v2_lite"):
+            if name == args.config:
+                continue
+            ocfg = CONFIGS[name]
+            log(f"[bench] building {name} (synthetic weights, seed 0)")
+            ow = make_weights(ocfg, seed=0, quant_device=dev)
+            olayer = build_block(ocfg, ow, device=dev)._layer
+            del ow
+            for tp in ocfg.runs.get("prefill", ()):
+                xp = make_inputs(ocfg, tp, seed=1).to(dev)
+                ms = time_events(lambda: olayer.forward(xp, want_logits=False), args.steps, args.warmup, stream)
+                tf = flops(ocfg, tp) / (ms * 1e-3) / 1e12
+                runs[f"{name}_prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4),
+                                                 "layer_tflops": round(tf, 1),
+                                                 "mfma_frac_layer": round(tf / PEAK_MFMA_F16_TFLOPS, 4)}
+            del olayer
+            torch.cuda.empty_cache()
     extra["runs"] = runs
 
     # ---------------- CPU baseline: oracle fp32 expert loop, bounded sample
@@ -205,6 +227,32 @@ def main():
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(line))
+
+
+def stack_run(cfg, layer, n_layers, T, args, stream):
+    """The n-layer stack of configs[4] at T-token prefill, timed end to end:
+    each layer's output feeds the next.  The layers share one set of synthetic
+    weights (581 MB, more than the 256 MB last-level cache, so every layer
+    still streams its experts from HBM)."""
+    import torch
+
+    from robustgemq_amd.synthetic import flops, make_inputs
+    dev = torch.device("cuda:0")
+    x0 = make_inputs(cfg, T, seed=4).to(dev)
+    bufs = [torch.empty_like(x0), torch.empty_like(x0)]
+
+    def stack():
+        h = x0
+        for i in range(n_layers):
+            layer.forward(h, out=bufs[i & 1], want_logits=False)
+            h = bufs[i & 1]
+
+    ms = time_events(stack, max(2, args.steps // 4), 1, stream)
+    tf = n_layers * flops(cfg, T) / (ms * 1e-3) / 1e12
+    return {f"mixtral_stack{n_layers}_prefill_T{T}": {
+        "tokens_per_s": round(T / (ms * 1e-3), 1), "ms": round(ms, 3), "layers": n_layers,
+        "tflops": round(tf, 1), "mfma_frac": round(tf / PEAK_MFMA_F16_TFLOPS, 4),
+        "weights": "one synthetic layer's weights reused by all layers"}}
 
 
 def decode_runs(cfg, layer, batches, args, stream, tag):
