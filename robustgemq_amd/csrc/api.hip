@@ -43,8 +43,15 @@ static Plan make_plan(const moeq_moe *m, int64_t T) {
   const double avg = double(p.pairs) / double(m->n_experts);
   p.bm = avg <= 16 ? 16 : avg <= 32 ? 32 : avg <= 64 ? 64 : 128;
   p.max_tiles = moeq_max_tiles(T, m->top_k, m->n_experts, m->n_shared, p.bm);
-  // 16-row (decode) blocks already split K over their waves
+  // 16-row (decode) down projections with few blocks also split K over
+  // work-groups (fp32 slices the combine adds in order), so enough waves keep
+  // weight fetches in flight: a K-split block of that shape covers 32 columns.
   p.splits = 1;
+  if (p.bm == 16) {
+    const int64_t blocks = int64_t(p.max_tiles) * cdiv(m->hidden, 32);
+    const int64_t nchunks = m->inter / 128;
+    if (blocks < 512) p.splits = int(std::max<int64_t>(1, std::min<int64_t>(cdiv(512, blocks), nchunks / 8)));
+  }
   p.y_dtype = p.splits > 1 ? MOEQ_F32 : MOEQ_F16;
   const int Et = m->n_experts + m->n_shared;
   size_t o = 0;

@@ -11,7 +11,7 @@ static int launch16(const GemmArgs &g, int max_tiles, int splits, hipStream_t s)
   using S = Shape<16, SILU>;
   const int64_t col_blocks = int64_t(max_tiles) * cdiv(g.N, tile_cols<S, false>());
   const int chunks = int(cdiv(g.nchunks, splits));
-  if (col_blocks < 512 || chunks > 32) return launch_one<16, SILU, ADT, ODT, true>(g, max_tiles, splits, s);
+  if (col_blocks < 256 || chunks > 32) return launch_one<16, SILU, ADT, ODT, true>(g, max_tiles, splits, s);
   return launch_one<16, SILU, ADT, ODT, false>(g, max_tiles, splits, s);
 }
 

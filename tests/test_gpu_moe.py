@@ -213,3 +213,91 @@ def test_reference_kernel_surface(device):
     assert relative_error(to_np(y).astype(np.float32), x.float().numpy() @ dense[1]) < 1e-3
     v = ops.dequant_splitk_gemv(x[:1].cuda(), words[2].cuda(), sc[2].cuda(), ze[2].cuda(), 3, g)
     assert relative_error(to_np(v).astype(np.float32), x[:1].float().numpy() @ dense[2]) < 1e-3
+
+
+# ------------------------------------------------------------- from_hf
+class _PackedLinear:
+    """Stand-in for a GemLite-converted linear: the five attributes from_hf
+    reads (moe_block.py:720-733) -- W_q [ceil(K/eps), N] int32 words,
+    scales / zeros [K/g, N] fp16 with zeros = z' (w = q*s + z')."""
+
+    def __init__(self, rng, N, K, bits, g, device):
+        self.codes = rng.integers(0, 1 << bits, size=(N, K)).astype(np.uint8)
+        s = (np.abs(rng.standard_normal((K // g, N))) * 0.004 + 5e-4).astype(np.float16)
+        zp = (rng.standard_normal((K // g, N)) * 0.004).astype(np.float16)
+        self.W_q = torch.from_numpy(oq.pack_cols(self.codes, bits)).to(device)
+        self.scales = torch.from_numpy(s).to(device)
+        self.zeros = torch.from_numpy(zp).to(device)
+        self.W_nbits, self.group_size = bits, g
+        gi = np.arange(K) // g
+        self.dense = oq.dequant_affine(self.codes.T.astype(np.float16), s[gi], zp[gi]).astype(np.float32).T.copy()
+
+
+class _Expert:
+    def __init__(self, rng, H, F, bits, g, device):
+        self.gate_proj = _PackedLinear(rng, F, H, bits, g, device)
+        self.up_proj = _PackedLinear(rng, F, H, bits, g, device)
+        self.down_proj = _PackedLinear(rng, H, F, bits, g, device)
+
+
+class _HFBlock(torch.nn.Module):
+    def __init__(self, rng, H, F, E, bits, g, n_shared, device):
+        super().__init__()
+        self.gate = torch.nn.Linear(H, E, bias=False).to(device=device, dtype=torch.float16)
+        with torch.no_grad():
+            self.gate.weight.copy_(torch.from_numpy((rng.standard_normal((E, H)) * 0.05).astype(np.float16)))
+        self.experts = [_Expert(rng, H, F, bits[e], g, device) for e in range(E)]
+        self.shared_experts = _Expert(rng, H, n_shared * F, 4, g, device) if n_shared else None
+
+
+@pytest.mark.parametrize("family,T", [("olmoe", 24), ("olmoe", 1), ("deepseekv2", 40), ("deepseekv2", 1)])
+def test_from_hf_gemlite_linears(device, family, T):
+    """from_hf, the constructor replace_moe_blocks calls (patch.py:86-162),
+    on GemLite-style expert linears: the stacked reference attributes and the
+    output against the oracle on q*s + z' weights."""
+    from robustgemq_amd.moe_block import BLOCKS
+    from robustgemq_amd.synthetic import _Cfg
+    _say(f"[from_hf] {family} T={T}")
+    rng = np.random.default_rng(11)
+    H, F, E, k, g = 512, 256, 8, 2, 64
+    bits = [1, 2, 3, 4, 2, 3, 4, 2]
+    n_sh = 2 if family == "deepseekv2" else 0
+    hf = _HFBlock(rng, H, F, E, bits, g, n_sh, "cuda")
+    common = dict(hidden_size=H, num_experts_per_tok=k, norm_topk_prob=False)
+    if family == "olmoe":
+        cfg = _Cfg(intermediate_size=F, num_experts=E, **common)
+    else:
+        cfg = _Cfg(moe_intermediate_size=F, n_routed_experts=E, n_shared_experts=n_sh, topk_method="greedy",
+                   scoring_func="softmax", routed_scaling_factor=1.0, **common)
+    block = BLOCKS[family].from_hf(cfg, hf)
+    # stacked reference attributes (moe_block.py:725-758)
+    assert torch.equal(block.w1_nbits.cpu(), torch.tensor(bits, dtype=torch.int32))
+    assert block.block_group_size == g
+    rows = [-(-H // (32 // b)) for b in bits]
+    assert block.w1_wq_strides.cpu().tolist() == list(np.cumsum([0] + [r * F for r in rows])[:-1])
+    assert torch.equal(block.w1_wq[:rows[0]], hf.experts[0].gate_proj.W_q)
+    if n_sh:
+        assert block.shared_nbits == 4 and block.shared_group_size == g
+    x = torch.from_numpy((rng.standard_normal((T, H)) * 0.5).astype(np.float16))
+    W1 = [e.gate_proj.dense for e in hf.experts]
+    W3 = [e.up_proj.dense for e in hf.experts]
+    W2 = [e.down_proj.dense for e in hf.experts]
+    shared = ()
+    if n_sh:
+        sh = hf.shared_experts
+        shared = ((sh.gate_proj.dense, sh.up_proj.dense, sh.down_proj.dense),)
+    gate = hf.gate.weight.detach().float().cpu().numpy()
+    ldt = "f32" if n_sh else "f16"
+    ref, ref_lg, ref_idx, _ = om.moe_forward(x.float().numpy(), gate, ldt, k, False, W1, W3, W2, shared)
+    res = block(x.cuda().reshape(1, T, H))
+    assert isinstance(res, tuple) == (family == "olmoe")
+    out = res[0] if isinstance(res, tuple) else res
+    got = to_np(out.reshape(T, H)).astype(np.float32)
+    out32, _ = block._layer.forward(x.cuda(), out_dtype=torch.float32, want_logits=False)
+    got32 = to_np(out32)
+    err, mx = relative_error(got32, ref), float(np.abs(got32 - ref).max())
+    _say(f"    rel-L2 {err:.3e} max-abs {mx:.3e} (|ref|max {np.abs(ref).max():.3e})")
+    assert err <= REL_L2 and mx <= MAX_ABS
+    assert relative_error(got, ref) <= REL_L2 and float(np.abs(got - ref).max()) <= MAX_ABS
+    if family == "olmoe" and T > 1:
+        np.testing.assert_array_equal(to_np(res[1]).astype(np.float32).view(np.uint32), ref_lg.view(np.uint32))
