@@ -168,10 +168,21 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
                              p.bm, counts, offsets, row_token, row_pair, inv, tiles, n_tiles, s);
     if (rc) return rc;
   } else {
-    rc = moeq_route(x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
-                    m->top_k, m->norm_topk, logits_out, idx, w, at(p.off_route),
-                    moeq_route_workspace_size(T, m->n_experts), stream);
-    if (rc) return rc;
+    // larger batches: fused logits + top-k (writing the fp16 copy of bf16
+    // activations on the way) where it covers the dtypes, else moeq_route
+    const int ldt = m->gate_dtype == MOEQ_F32 ? MOEQ_F32 : m->act_dtype;
+    RouteArgs ra{x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
+                 m->top_k, m->norm_topk ? 1 : 0, logits_out, ldt, ldt, idx, w,
+                 m->act_dtype == MOEQ_BF16 ? static_cast<uint16_t *>(at(p.off_x16)) : nullptr};
+    if (m->hidden % 8 == 0 && m->hidden <= 4096 && launch_logits_topk(ra, as_stream(stream))) {
+      if ((rc = check_launch("moe/logits_topk"))) return rc;
+      x16_done = m->act_dtype == MOEQ_BF16;
+    } else {
+      rc = moeq_route(x, m->act_dtype, T, m->hidden, m->gate_w, m->gate_dtype, m->logit_bias, m->n_experts,
+                      m->top_k, m->norm_topk, logits_out, idx, w, at(p.off_route),
+                      moeq_route_workspace_size(T, m->n_experts), stream);
+      if (rc) return rc;
+    }
     rc = moeq_permute(idx, T, m->top_k, m->n_experts, m->n_shared, p.bm, counts, offsets, row_token,
                       row_pair, inv, tiles, n_tiles, at(p.off_perm),
                       moeq_permute_workspace_size(T, m->top_k, m->n_experts, m->n_shared), stream);

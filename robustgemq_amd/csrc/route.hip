@@ -31,6 +31,247 @@ __global__ __launch_bounds__(256) void topk_from_logits_kernel(
   select_topk<EREG>(vals, E, k, norm, t, idx, w);
 }
 
+// ---------------------------------------------------------------- prefill
+// Logits and top-k of 8 tokens per work-group.  Wave w takes 8-expert blocks
+// w, w + NWV, ...; each lane runs the 64 chains of an 8 x 8 (token, expert)
+// block over its k set, so every loaded x / w value feeds 8 fused
+// multiply-adds.  The 64 chains are then summed over the lanes by halving
+// exchanges that pair the same lanes in the same order as the xor butterfly
+// (o = 32 .. 1), leaving chain l in lane l with the identical value.  The
+// rounded logits of the 8 tokens meet in LDS, and one wave per token ranks
+// them.
+constexpr int kTT = 8, kEE = 8;
+
+// One operand row: the 8 values of one k step, as loaded (fp16 / bf16: four
+// packed words; fp32: eight words).
+template <int DT>
+struct Raw8 {
+  static constexpr int W = DT == MOEQ_F32 ? 8 : 4;
+  uint32_t u[W];
+  // 8 values at byte offset voff (per lane) + soff (uniform) of the buffer
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0);
+    u[0] = a[0]; u[1] = a[1]; u[2] = a[2]; u[3] = a[3];
+    if constexpr (W == 8) {
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff + 16), int(soff), 0);
+      u[4] = b[0]; u[5] = b[1]; u[6] = b[2]; u[7] = b[3];
+    }
+  }
+  // value j widened to fp32 (exact)
+  __device__ __forceinline__ float value(int j) const {
+    if constexpr (DT == MOEQ_F32) return __uint_as_float(u[j]);
+    else if constexpr (DT == MOEQ_BF16) return __uint_as_float((j & 1) ? (u[j >> 1] & 0xffff0000u) : (u[j >> 1] << 16));
+    else return f16_bits_to_f32(uint16_t(u[j >> 1] >> (16 * (j & 1))));
+  }
+};
+
+// fmaf(x_j, w_j, c) with one rounding.  fp16 operands go to v_fma_mix_f32
+// straight from the packed word (the widening is exact); other operands are
+// widened first (xf / wf: value j of the row, precomputed by the caller).
+template <int XDT, int WDT>
+__device__ __forceinline__ float fma_j(const Raw8<XDT> &x, float xf, const Raw8<WDT> &w, float wf, int j, float c) {
+  float r;
+  if constexpr (XDT == MOEQ_F16 && WDT == MOEQ_F16) {
+    if (j & 1)
+      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(x.u[j >> 1]), "v"(w.u[j >> 1]), "v"(c));
+    else
+      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(x.u[j >> 1]), "v"(w.u[j >> 1]), "v"(c));
+  } else if constexpr (XDT == MOEQ_F16 && WDT == MOEQ_F32) {
+    if (j & 1)
+      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x.u[j >> 1]), "v"(w.u[j]), "v"(c));
+    else
+      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x.u[j >> 1]), "v"(w.u[j]), "v"(c));
+  } else {
+    r = __builtin_fmaf(xf, wf, c);
+  }
+  return r;
+}
+
+// Sum of chain c[j] over the 64 lanes, for all 64 j at once; lane l returns
+// the sum of chain l.  Level o keeps, in each lane, the half of the chains
+// whose bit matches the lane's bit o and adds the partner's (lane ^ o) copy:
+// the pairs are those of the butterfly v <- v + v[lane ^ o] (fp32 addition
+// commutes), so every sum is identical to the butterfly's.  Levels 32 and 16
+// are one v_permlane32/16_swap per pair of chains: after swapping c[j]'s
+// upper half (odd rows) with c[j + o]'s lower half (even rows), the two
+// registers hold, lane by lane, the kept value and its partner.
+__device__ __forceinline__ float halving_sum(float (&c)[64]) {
+  const int lane = lane_id();
+  float a[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(c[j]), __float_as_uint(c[j + 32]), false, false);
+    a[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[j]), __float_as_uint(a[j + 16]), false, false);
+    a[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) {
+    const bool up = lane & o;
+#pragma unroll
+    for (int j = 0; j < o; ++j) {
+      const float send = up ? a[j] : a[j + o], keep = up ? a[j + o] : a[j];
+      a[j] = keep + __shfl_xor(send, o);
+    }
+  }
+  return a[0];
+}
+
+template <int XDT, int WDT, int NWV, int MAXCH>
+__global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
+  __shared__ float lg[kTT][512];
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int64_t t0 = int64_t(blockIdx.x) * kTT;
+  const int n_eb = (a.E + kEE - 1) / kEE;
+  // two k steps in flight for fp16 rows; widened operands need the registers
+  constexpr int NBUF = (XDT == MOEQ_F16 && WDT == MOEQ_F16) ? 2 : 1;
+  for (int eb = wave; eb < n_eb; eb += NWV) {
+    const int e0 = eb * kEE;
+    float ch[kTT * kEE];
+#pragma unroll
+    for (int i = 0; i < kTT * kEE; ++i) ch[i] = 0.f;
+    // Rows are read through buffer resources based at this block's first
+    // token / expert: one 32-bit lane offset (the k position) serves all 16
+    // rows, whose row offsets are uniform.  Rows past T or E, and k steps past
+    // H, load a valid row (token T - 1, expert E - 1, k = H - 8) that is never
+    // used, so the loads are unconditional.
+    constexpr uint32_t XES = XDT == MOEQ_F32 ? 4 : 2, WES = WDT == MOEQ_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char *>(static_cast<const char *>(a.x) + t0 * a.H * XES), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char *>(static_cast<const char *>(a.wg) + int64_t(e0) * a.H * WES), (short)0, 0x7fffffff,
+        0x00020000);
+    auto fetch = [&](int i, Raw8<XDT> (&xb)[kTT], Raw8<WDT> (&wb)[kEE]) {
+      const uint32_t kc = uint32_t(min(512 * i + 8 * lane, a.H - 8));
+#pragma unroll
+      for (int tt = 0; tt < kTT; ++tt)
+        xb[tt].load(xrs, kc * XES, uint32_t(min(int64_t(tt), a.T - 1 - t0)) * uint32_t(a.H) * XES);
+#pragma unroll
+      for (int ee = 0; ee < kEE; ++ee)
+        wb[ee].load(wrs, kc * WES, uint32_t(min(ee, a.E - 1 - e0)) * uint32_t(a.H) * WES);
+    };
+    auto step = [&](int i, const Raw8<XDT> (&xb)[kTT], const Raw8<WDT> (&wb)[kEE]) {
+      const int k0 = 512 * i + 8 * lane;
+      if (k0 >= a.H) return;
+      if (a.x16 && eb == 0) {  // the activations the expert GEMMs read, converted once
+#pragma unroll
+        for (int tt = 0; tt < kTT; ++tt) {
+          if (t0 + tt >= a.T) continue;
+          uint32_t h[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            h[j] = uint32_t(f32_to_f16_bits(xb[tt].value(2 * j))) |
+                   (uint32_t(f32_to_f16_bits(xb[tt].value(2 * j + 1))) << 16);
+          *reinterpret_cast<uint4 *>(a.x16 + (t0 + tt) * a.H + k0) = (uint4){h[0], h[1], h[2], h[3]};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float xf[kTT], wf[kEE];
+#pragma unroll
+        for (int tt = 0; tt < kTT; ++tt) xf[tt] = XDT == MOEQ_F16 ? 0.f : xb[tt].value(j);
+#pragma unroll
+        for (int ee = 0; ee < kEE; ++ee) wf[ee] = XDT == MOEQ_F16 ? 0.f : wb[ee].value(j);
+        // rows past T / E hold data of another row: their chains are never stored
+#pragma unroll
+        for (int tt = 0; tt < kTT; ++tt)
+#pragma unroll
+          for (int ee = 0; ee < kEE; ++ee)
+            ch[tt * kEE + ee] = fma_j<XDT, WDT>(xb[tt], xf[tt], wb[ee], wf[ee], j, ch[tt * kEE + ee]);
+      }
+    };
+    if constexpr (NBUF == 2) {
+      // k steps i (rows A) and i + 1 (rows B) per trip: the next step's rows
+      // are in flight while one step is multiplied
+      Raw8<XDT> xa[kTT], xb[kTT];
+      Raw8<WDT> wa[kEE], wb[kEE];
+      fetch(0, xa, wa);
+#pragma unroll 1
+      for (int i = 0; i < MAXCH; i += 2) {
+        fetch(i + 1, xb, wb);
+        __builtin_amdgcn_sched_barrier(0);
+        step(i, xa, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(i + 2, xa, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < MAXCH) step(i + 1, xb, wb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      Raw8<XDT> xa[kTT];
+      Raw8<WDT> wa[kEE];
+#pragma unroll 1
+      for (int i = 0; i < MAXCH; ++i) {
+        fetch(i, xa, wa);
+        step(i, xa, wa);
+      }
+    }
+    float v = halving_sum(ch);
+    const int tt = lane / kEE, e = e0 + lane % kEE;
+    const int64_t t = t0 + tt;
+    if (e < a.E) {
+      if (a.bias) v = v + a.bias[e];
+      v = round_logit(v, a.logits_dtype);
+      lg[tt][e] = v;
+      if (a.logits && t < a.T) store_logit(a.logits, a.store_dtype, t * a.E + e, v);
+    }
+  }
+  __syncthreads();
+  for (int tt = wave; tt < kTT && t0 + tt < a.T; tt += NWV) {
+    const int ereg = ereg_for(a.E);
+#define MOEQ_SEL(R)                                                       \
+  {                                                                       \
+    float vals[R];                                                        \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                       \
+      const int e = 64 * r + lane;                                        \
+      vals[r] = e < a.E ? lg[tt][e] : -INFINITY;                          \
+    }                                                                     \
+    select_topk<R>(vals, a.E, a.k, a.norm, t0 + tt, a.idx, a.w);          \
+  }
+    if (ereg == 1) MOEQ_SEL(1) else if (ereg == 2) MOEQ_SEL(2) else if (ereg == 4) MOEQ_SEL(4) else MOEQ_SEL(8)
+#undef MOEQ_SEL
+  }
+}
+
+template <int XDT, int WDT, int NWV>
+static void launch_logits_topk_nw(const RouteArgs &a, int maxch, hipStream_t s) {
+  dim3 grid(unsigned(cdiv(a.T, kTT))), block(NWV * 64);
+  switch (maxch) {
+    case 1: logits_topk_kernel<XDT, WDT, NWV, 1><<<grid, block, 0, s>>>(a); break;
+    case 2: logits_topk_kernel<XDT, WDT, NWV, 2><<<grid, block, 0, s>>>(a); break;
+    case 4: logits_topk_kernel<XDT, WDT, NWV, 4><<<grid, block, 0, s>>>(a); break;
+    default: logits_topk_kernel<XDT, WDT, NWV, 8><<<grid, block, 0, s>>>(a); break;
+  }
+}
+
+template <int XDT, int WDT>
+static void launch_logits_topk_dt(const RouteArgs &a, int maxch, hipStream_t s) {
+  if (a.E <= 8) launch_logits_topk_nw<XDT, WDT, 1>(a, maxch, s);
+  else if (a.E <= 16) launch_logits_topk_nw<XDT, WDT, 2>(a, maxch, s);
+  else if (a.E <= 32) launch_logits_topk_nw<XDT, WDT, 4>(a, maxch, s);
+  else launch_logits_topk_nw<XDT, WDT, 8>(a, maxch, s);
+}
+
+// Fused logits + top-k for batches above T * E = 16384; returns false (and
+// launches nothing) for a dtype pair it does not cover.
+bool launch_logits_topk(const RouteArgs &a, hipStream_t s) {
+  if (a.T * a.E <= 16384 || a.E > 512 || a.k > kMaxTopK || a.H % 8 || a.H > 4096) return false;
+  const int maxch = a.H <= 512 ? 1 : a.H <= 1024 ? 2 : a.H <= 2048 ? 4 : 8;
+  const int x = a.x_dtype, w = a.wg_dtype;
+  if (x == MOEQ_F16 && w == MOEQ_F16) launch_logits_topk_dt<MOEQ_F16, MOEQ_F16>(a, maxch, s);
+  else if (x == MOEQ_F16 && w == MOEQ_F32) launch_logits_topk_dt<MOEQ_F16, MOEQ_F32>(a, maxch, s);
+  else if (x == MOEQ_BF16 && w == MOEQ_BF16) launch_logits_topk_dt<MOEQ_BF16, MOEQ_BF16>(a, maxch, s);
+  else if (x == MOEQ_BF16 && w == MOEQ_F32) launch_logits_topk_dt<MOEQ_BF16, MOEQ_F32>(a, maxch, s);
+  else if (x == MOEQ_F32 && w == MOEQ_F32) launch_logits_topk_dt<MOEQ_F32, MOEQ_F32>(a, maxch, s);
+  else return false;
+  return true;
+}
+
 template <int TT, int EE>
 static void launch_logits(const RouteArgs &a, int maxch, hipStream_t s) {
   const int n_et = int(cdiv(a.E, EE));
@@ -95,6 +336,13 @@ extern "C" int moeq_route(const void *x, int x_dtype, int64_t T, int H,
   if (top_k <= 0 || top_k > E || top_k > kMaxTopK)
     return fail(MOEQ_ERR_INVALID, "route: top_k=%d must be in 1..min(n_experts=%d, %d)", top_k, E, kMaxTopK);
   const int ldt = gate_dtype == MOEQ_F32 ? MOEQ_F32 : x_dtype;
+  hipStream_t s = as_stream(stream);
+  {
+    // batches above 16384 logits: one fused launch, logits stored only if asked
+    RouteArgs f{x, x_dtype, T, H, gate_w, gate_dtype, logit_bias, E, top_k, norm_topk ? 1 : 0,
+                logits_out, ldt, ldt, idx_out, w_out};
+    if (launch_logits_topk(f, s)) return check_launch("route/logits_topk");
+  }
   void *lg = logits_out;
   int lg_dt = ldt;
   if (!lg) {
@@ -106,7 +354,6 @@ extern "C" int moeq_route(const void *x, int x_dtype, int64_t T, int H,
   }
   RouteArgs a{x, x_dtype, T, H, gate_w, gate_dtype, logit_bias, E, top_k, norm_topk ? 1 : 0,
               lg, ldt, lg_dt, idx_out, w_out};
-  hipStream_t s = as_stream(stream);
   int rc = launch_route_logits(a, s);
   if (rc) return rc;
   // the selection reads the rounded logits (stored as ldt, or exactly as fp32)

@@ -67,64 +67,61 @@ __device__ __forceinline__ void load8(const void *p, int dtype, int64_t i, float
 }
 
 // Top-k of the logits held by one wave (expert e = 64 r + lane in vals[r]),
-// ranked by value with ties to the lower index; softmax weights over all E
-// experts; optional renormalisation over the selected k.  Writes row t.
+// ranked by value with ties to the lower index (NaN ranks last); softmax
+// weights over all E experts; optional renormalisation over the selected k.
+// Writes row t.  Each expert's rank is counted directly: every value is
+// broadcast once (v_readlane) and compared with all of them, so there is no
+// sequential select-and-remove loop and no dynamically indexed register.
 template <int EREG>
 __device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
                             int64_t t, int32_t *idx_out, float *w_out) {
   const int lane = lane_id();
-  bool avail[EREG];
 #pragma unroll
   for (int r = 0; r < EREG; ++r) {
-    int e = 64 * r + lane;
-    avail[r] = e < E;
-    if (!avail[r] || vals[r] != vals[r]) vals[r] = -INFINITY;  // NaN ranks last
+    const int e = 64 * r + lane;
+    if (e >= E || vals[r] != vals[r]) vals[r] = -INFINITY;  // NaN ranks last
   }
-  int sel_i[kMaxTopK];
-  float sel_v[kMaxTopK];
-  for (int s = 0; s < k; ++s) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+  int rank[EREG];
 #pragma unroll
-    for (int r = 0; r < EREG; ++r) {
-      int e = 64 * r + lane;
-      if (avail[r] && (vals[r] > bv || (vals[r] == bv && e < bi))) {
-        bv = vals[r];
-        bi = e;
+  for (int r = 0; r < EREG; ++r) rank[r] = 0;
+  float m = -INFINITY;
+#pragma unroll
+  for (int r2 = 0; r2 < EREG; ++r2) {
+    if (64 * r2 >= E) break;
+#pragma unroll 16
+    for (int l2 = 0; l2 < 64; ++l2) {
+      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vals[r2]), l2));
+      const int e2 = 64 * r2 + l2;
+      m = fmaxf(m, v);
+#pragma unroll
+      for (int r = 0; r < EREG; ++r) {
+        const int e = 64 * r + lane;
+        rank[r] += (v > vals[r] || (v == vals[r] && e2 < e)) ? 1 : 0;
       }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      float ov = __shfl_xor(bv, o);
-      int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    sel_i[s] = bi;
-    sel_v[s] = bv;
-#pragma unroll
-    for (int r = 0; r < EREG; ++r)
-      if (64 * r + lane == bi) avail[r] = false;
   }
-  const float m = sel_v[0];
+  // m is the top value (sel 0) unless every logit is -inf / NaN
   float den = 0.f;
 #pragma unroll
   for (int r = 0; r < EREG; ++r)
     if (64 * r + lane < E) den += __expf(vals[r] - m);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o);
-  float p[kMaxTopK];
+  float p[EREG];
   float psum = 0.f;
-  for (int s = 0; s < k; ++s) {
-    p[s] = __expf(sel_v[s] - m) / den;
-    psum += p[s];
+#pragma unroll
+  for (int r = 0; r < EREG; ++r) {
+    p[r] = __expf(vals[r] - m) / den;
+    if (64 * r + lane < E && rank[r] < k) psum += p[r];
   }
-  for (int s = 0; s < k; ++s) {
-    if (lane == s) {
-      idx_out[t * k + s] = sel_i[s];
-      w_out[t * k + s] = norm ? p[s] / psum : p[s];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) psum += __shfl_xor(psum, o);
+#pragma unroll
+  for (int r = 0; r < EREG; ++r) {
+    const int e = 64 * r + lane;
+    if (e < E && rank[r] < k) {
+      idx_out[t * k + rank[r]] = e;
+      w_out[t * k + rank[r]] = norm ? p[r] / psum : p[r];
     }
   }
 }
@@ -201,11 +198,17 @@ __device__ void logit_tile(const RouteArgs &a, int64_t t0, int e0) {
     }
 }
 
-static inline int ereg_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
+__host__ __device__ inline int ereg_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 8; }
 
 // Logits of every (token, expert) pair (rounded as RouteArgs asks), without
 // the selection; defined in route.hip.
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
+
+// Logits (stored only when a.logits is set) and top-k in one launch, for
+// T * E > 16384 and the dtype pairs (x, gate) f16/f16, f16/f32, bf16/bf16,
+// bf16/f32, f32/f32; returns false without launching otherwise.  Needs
+// H % 8 == 0 and H <= 4096, E <= 512 (route.hip).
+bool launch_logits_topk(const RouteArgs &a, hipStream_t s);
 
 // Top-k of T rows of logits followed by the token -> expert permutation, in
 // one work-group; valid when T * k <= kFusedPairs and E + n_shared <=
