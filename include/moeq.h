@@ -137,13 +137,19 @@ int moeq_route_from_logits(const void *logits, int dtype, int64_t T, int E,
  *   row_pair[T*top_k]                t*top_k + slot of each routed row,
  *   inv_perm[T*top_k]                row of each (t, slot) pair,
  *   tiles[max_tiles*4]               (expert, row_start, row_count, 0): each
- *                                    expert's rows as full `bm`-row tiles
- *                                    plus one remainder tile, in expert order,
+ *                                    expert's m rows split into
+ *                                    ceil(m / moeq_tile_rows(bm)) tiles of
+ *                                    near-equal size (counts differ by at
+ *                                    most one), in expert order,
  *   n_tiles[1].
  * max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm).
  * Replaces the one_hot / nonzero / torch.where grouping and its host syncs,
  * gemq/inference/moe_block.py:803-810 (also :256-262, :562-570, :1033-1040). */
 int moeq_max_tiles(int64_t T, int top_k, int E, int n_shared, int bm);
+/* Most rows one tile of tile class bm holds (the schedule's split size and
+ * the grouped GEMM's row capacity): 16 -> 16, 32 -> 48, 64 -> 96,
+ * 128 -> 160, 256 -> 256; 0 for any other bm.  No reference counterpart. */
+int moeq_tile_rows(int bm);
 size_t moeq_permute_workspace_size(int64_t T, int top_k, int E, int n_shared);
 int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
                  int n_shared, int bm, int32_t *counts, int32_t *offsets,
@@ -164,7 +170,8 @@ typedef struct moeq_gemm {
   const int32_t *tiles;     /* from moeq_permute (or built by the caller)    */
   const int32_t *n_tiles;   /* device scalar                                 */
   int32_t max_tiles;        /* host bound on *n_tiles                        */
-  int32_t bm;               /* tile height the schedule was built for: 16, 32, 64 or 128 */
+  int32_t bm;               /* tile class the schedule was built for: 16, 32, 64, 128 or 256;
+                               every tile holds at most moeq_tile_rows(bm) rows */
   int32_t epilogue;         /* MOEQ_EPI_*                                    */
   void *out;                /* [rows, N] (split s at out + s*split_stride)   */
   int32_t out_dtype;        /* MOEQ_F16 | MOEQ_F32 (split-K needs F32)       */

@@ -89,6 +89,7 @@ SIGNATURES = {
     "moeq_route_from_logits": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p,
                                        c_void_p, c_void_p]),
     "moeq_max_tiles": (c_int, [c_int64, c_int, c_int, c_int, c_int]),
+    "moeq_tile_rows": (c_int, [c_int]),
     "moeq_permute_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int]),
     "moeq_permute": (c_int, [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,

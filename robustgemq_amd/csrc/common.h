@@ -25,6 +25,14 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Row capacity of one grouped-GEMM tile of class bm: the schedule splits an
+// expert's m rows into ceil(m / cap) near-equal tiles, so the prefill classes
+// leave room above their nominal height (an expert a little past 2 x 128 rows
+// still takes two tiles, not three).  0 for an unknown class.
+__host__ __device__ constexpr int tile_rows(int bm) {
+  return bm == 16 ? 16 : bm == 32 ? 48 : bm == 64 ? 96 : bm == 128 ? 160 : bm == 256 ? 256 : 0;
+}
+
 // ------------------------------------------------------- device helpers
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(uint32_t(b) << 16);

@@ -3,9 +3,9 @@
 // instantiates one row-tile height BM.
 //
 // One launch covers every (row tile, column tile) of every expert; the row
-// tiles come from the device-side schedule written by moeq_permute (full BM
-// tiles plus one remainder tile per expert), so no host synchronisation is
-// needed.  A block has NW waves; wave w owns NB * 16 output columns and all
+// tiles come from the device-side schedule written by moeq_permute (each
+// expert's rows in near-equal tiles of at most tile_rows(BM) rows), so no
+// host synchronisation is needed.  A block has NW waves; wave w owns NB * 16 output columns and all
 // active rows of the tile.  Per 128-deep K chunk:
 //   A (activations, gathered rows): BM >= 32 -> copied global -> LDS with
 //      buffer_load_dwordx4 ... lds (no register staging), 16-byte units XOR-
@@ -155,7 +155,7 @@ template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, i
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, int mcount, int nt,
                                           int c0, int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {
   constexpr int NT = NW * 64;
-  static_assert(MBA * 16 <= BM, "active row blocks exceed the tile");
+  static_assert(MBA * 16 <= tile_rows(BM), "active row blocks exceed the tile");
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, kb = lane >> 4;
@@ -427,19 +427,20 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
   if constexpr (BM == 16) {
     MOEQ_T(1);
   } else if constexpr (BM == 32) {
-    MOEQ_T(2);
+    if (mb_act <= 2) MOEQ_T(2); else MOEQ_T(3);
   } else if constexpr (BM == 64) {
-    if (mb_act <= 2) MOEQ_T(2); else MOEQ_T(4);
+    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else MOEQ_T(6);
   } else if constexpr (BM == 128) {
-    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else MOEQ_T(8);
+    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else if (mb_act <= 8) MOEQ_T(8); else MOEQ_T(10);
   } else {
     if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else if (mb_act <= 8) MOEQ_T(8); else MOEQ_T(16);
   }
 #undef MOEQ_T
 }
 
-// Two work-groups per CU for the 32..128-row shapes and one 8-wave group for
-// the 256-row shape (its two A buffers take 128 KB of LDS): 2 waves per SIMD.
+// Two work-groups per CU for the 32..128 classes (tiles of up to 48..160
+// rows) and one 8-wave group for the 256-row shape (its two A buffers take
+// 128 KB of LDS): 2 waves per SIMD.
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, bool KS>
 __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
   // The grid is sized for the host-side bound on row tiles; blocks past the
@@ -455,9 +456,11 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
   // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * NB * 4
-  // floats per lane, at most 12 KB
-  __shared__ uint4 As0[BM == 16 ? 48 : BM][16];
-  __shared__ uint4 As1[BM == 16 ? 1 : BM][16];
+  // floats per lane, at most 12 KB.  The prefill classes hold tile_rows(BM)
+  // rows per buffer (two 40 KB buffers for the 160-row class: two
+  // work-groups fill the 160 KB of LDS).
+  __shared__ uint4 As0[BM == 16 ? 48 : tile_rows(BM)][16];
+  __shared__ uint4 As1[BM == 16 ? 1 : tile_rows(BM)][16];
   const int32_t *tp = g.tiles + 4 * mt;
   const int e = tp[0], row0 = tp[1], mcount = tp[2];
   const int c0 = int(blockIdx.z) * g.chunks_per_split;

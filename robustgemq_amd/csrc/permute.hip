@@ -92,9 +92,10 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
                         int32_t *n_tiles, int *sh, int *s_off) {
   const int e = threadIdx.x, Et = E + n_shared;
   const int m = e < Et ? c : 0;
-  // an expert's full tiles, then its remainder tile; experts in order, so
-  // the tiles sharing an expert's weights are dispatched together
-  const int nt = (m + bm - 1) / bm;
+  // an expert's rows in ceil(m / cap) tiles of near-equal size; experts in
+  // order, so the tiles sharing an expert's weights are dispatched together
+  const int cap = tile_rows(bm);
+  const int nt = (m + cap - 1) / cap;
   int tot_rows, tot_tiles;
   const int off = block_exclusive_scan(m, sh, &tot_rows);
   const int tb = block_exclusive_scan(nt, sh, &tot_tiles);
@@ -110,10 +111,11 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
     *n_tiles = min(tot_tiles, max_tiles);
   }
   for (int j = 0; j < nt && tb + j < max_tiles; ++j) {
+    const int r0 = int(int64_t(m) * j / nt), r1 = int(int64_t(m) * (j + 1) / nt);
     int32_t *tp = tiles + 4 * (tb + j);
     tp[0] = e;
-    tp[1] = off + j * bm;
-    tp[2] = min(bm, m - j * bm);
+    tp[1] = off + r0;
+    tp[2] = r1 - r0;
     tp[3] = 0;
   }
   __syncthreads();
@@ -357,10 +359,14 @@ int launch_topk_permute(const void *logits, int dtype, int64_t T, int E, int k, 
 
 using namespace moeq;
 
+extern "C" int moeq_tile_rows(int bm) { return tile_rows(bm); }
+
 extern "C" int moeq_max_tiles(int64_t T, int top_k, int E, int n_shared, int bm) {
-  if (T <= 0 || top_k <= 0 || E <= 0 || n_shared < 0 || bm <= 0) return 0;
+  const int cap = tile_rows(bm);
+  if (T <= 0 || top_k <= 0 || E <= 0 || n_shared < 0 || cap <= 0) return 0;
+  // sum over experts of ceil(m_e / cap) <= pairs / cap + (experts with rows)
   int64_t pairs = T * top_k;
-  int64_t bound = pairs / bm + std::min<int64_t>(E, pairs) + int64_t(n_shared) * cdiv(T, bm);
+  int64_t bound = pairs / cap + std::min<int64_t>(E, pairs) + int64_t(n_shared) * cdiv(T, cap);
   return int(bound);
 }
 
@@ -381,7 +387,7 @@ extern "C" int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
   if (E <= 0 || n_shared < 0 || E + n_shared > kMaxExperts)
     return fail(MOEQ_ERR_UNSUPPORTED, "permute: n_experts=%d + n_shared=%d exceeds %d", E, n_shared, kMaxExperts);
   if (top_k > E) return fail(MOEQ_ERR_INVALID, "permute: top_k=%d > n_experts=%d", top_k, E);
-  if (bm < 16 || bm % 16) return fail(MOEQ_ERR_INVALID, "permute: bm=%d must be a positive multiple of 16", bm);
+  if (tile_rows(bm) == 0) return fail(MOEQ_ERR_INVALID, "permute: bm=%d not in {16, 32, 64, 128, 256}", bm);
   if (T * top_k > INT32_MAX / 2 || T * (top_k + n_shared) > INT32_MAX / 2)
     return fail(MOEQ_ERR_UNSUPPORTED, "permute: T=%lld too large", (long long)T);
   size_t need = moeq_permute_workspace_size(T, top_k, E, n_shared);

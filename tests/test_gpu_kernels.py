@@ -110,11 +110,20 @@ def test_permute_bit_exact(device, T, k, E, S, bm):
     assert 0 < nt <= out["max_tiles"]
     tiles = to_np(out["tiles"])[:nt]
     covered = np.zeros(T * k + S * T, np.int32)
+    cap = ops.L.lib().moeq_tile_rows(bm)
     for e, r0, rc, _ in tiles:
-        assert 0 < rc <= bm
+        assert 0 < rc <= cap
         assert ref["offsets"][e] <= r0 and r0 + rc <= ref["offsets"][e + 1]
         covered[r0:r0 + rc] += 1
     assert (covered == 1).all()
+    # each expert's m rows in ceil(m / cap) tiles whose sizes differ by at most one
+    sizes = {}
+    for e, r0, rc, _ in tiles:
+        sizes.setdefault(int(e), []).append(int(rc))
+    for e, m in enumerate(ref["counts"]):
+        got = sizes.get(e, [])
+        assert len(got) == -(-int(m) // cap), (e, m, got)
+        assert not got or max(got) - min(got) <= 1, (e, m, got)
 
 
 # ------------------------------------------------------------- grouped GEMM
@@ -168,10 +177,11 @@ def test_grouped_gemm_store_matches_fp32(device, bm, mode, g):
     T = 61
     x = (rng.standard_normal((T, K)) * 0.5).astype(np.float16)
     row_src = rng.integers(0, T, size=rows).astype(np.int32)
+    cap = ops.L.lib().moeq_tile_rows(bm)  # tiles as tall as the class holds
     tiles, r = [], 0
     for e, m in enumerate(counts):
-        for j in range(0, m, bm):
-            tiles.append((e, r + j, min(bm, m - j), 0))
+        for j in range(0, m, cap):
+            tiles.append((e, r + j, min(cap, m - j), 0))
         r += m
     tt = torch.tensor(tiles, dtype=torch.int32, device=device)
     n = torch.tensor([len(tiles)], dtype=torch.int32, device=device)
@@ -231,10 +241,11 @@ def test_grouped_gemm_silu_mul_and_splitk(device, bm, adt):
     counts = [40, 7, 130]
     rows = sum(counts)
     x = torch.from_numpy((rng.standard_normal((rows, K)) * 0.5).astype(np.float32)).to(adt)
+    cap = ops.L.lib().moeq_tile_rows(bm)  # tiles as tall as the class holds
     tiles, r = [], 0
     for e, m in enumerate(counts):
-        for j in range(0, m, bm):
-            tiles.append((e, r + j, min(bm, m - j), 0))
+        for j in range(0, m, cap):
+            tiles.append((e, r + j, min(cap, m - j), 0))
         r += m
     tt = torch.tensor(tiles, dtype=torch.int32, device=device)
     n = torch.tensor([len(tiles)], dtype=torch.int32, device=device)

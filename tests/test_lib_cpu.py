@@ -126,6 +126,8 @@ def test_max_tiles_bounds_every_routing():
     for T, k, E, S, bm in ((1, 8, 64, 0, 16), (7, 2, 8, 0, 16), (2048, 8, 64, 0, 128), (2048, 6, 64, 2, 128),
                            (300, 6, 64, 2, 32), (33, 8, 64, 0, 64)):
         bound = lib.moeq_max_tiles(T, k, E, S, bm)
+        cap = lib.moeq_tile_rows(bm)
+        assert cap >= bm
         for skew in (0.0, 3.0):
             p = np.exp(-skew * np.arange(E) / E)
             p /= p.sum()
@@ -133,9 +135,15 @@ def test_max_tiles_bounds_every_routing():
             counts = list(np.bincount(idx.reshape(-1), minlength=E)) + [T] * S
             tiles = 0
             for m in counts:
-                tiles += -(-m // bm)
+                tiles += -(-m // cap)
             assert tiles <= bound, (T, k, E, S, bm, tiles, bound)
         assert permute  # imported for parity of the tile rule with the oracle grouping
+
+
+def test_tile_rows_classes():
+    lib = L.lib()
+    assert [lib.moeq_tile_rows(b) for b in (16, 32, 64, 128, 256)] == [16, 48, 96, 160, 256]
+    assert lib.moeq_tile_rows(48) == 0 and lib.moeq_tile_rows(0) == 0
 
 
 def test_layer_plan_and_workspace():
