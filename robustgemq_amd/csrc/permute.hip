@@ -2,15 +2,18 @@
 //
 // The pairs (t, slot) are visited in slot-major order p = slot * T + t, the
 // order torch.where walks the [k, T] expert mask in the reference, and stably
-// sorted by expert:
-//   1. hist:    one wave per chunk of kChunk positions counts experts (LDS).
-//   2. scan:    one block turns the chunk counts into per-(chunk, expert)
-//               start rows, expert offsets and the row-tile schedule, and
-//               writes the rows of the shared experts.
-//   3. scatter: one wave per chunk walks its positions in order, 64 at a
-//               time; lanes with the same expert are found with one ballot
-//               per key bit, ranked by lane order, and placed after the
-//               rows already emitted for that expert.
+// sorted by expert.  Three paths by batch size (E + n_shared <= 256 for the
+// first two):
+//   * up to 4096 pairs: one work-group holds every expert id in registers,
+//     counts, scans and places them (permute_block);
+//   * up to 65536 pairs: one work-group per 512 positions counts its chunk
+//     (chunk_hist), then every work-group sums the chunk counts itself and
+//     places its chunk (chunk_scatter);
+//   * beyond: hist (one wave per chunk), scan (one block turns the chunk
+//     counts into per-(chunk, expert) start rows), scatter.
+// Placing 64 pairs at a time: lanes with the same expert are found with one
+// ballot per key bit, ranked by lane order, and put after the rows already
+// emitted for that expert.
 #include <algorithm>
 
 #include "routing.h"
@@ -218,13 +221,17 @@ __device__ __forceinline__ void peer_rank(bool valid, int e, int key_bits, int *
   *leader = valid && (peers >> lane) == 1ull;
 }
 
-// Everything in one work-group (16 waves) for up to kFusedPairs pairs: each
-// wave counts a contiguous slice of the slot-major sequence, the block scans
-// the counts into slice bases, then each wave places its slice in order.
+// Everything in one work-group (16 waves) for up to kFusedPairs pairs: wave
+// w owns the slice [w * 64 * PPL, (w + 1) * 64 * PPL) of the slot-major
+// sequence and loads all its expert ids into registers at once (one memory
+// round trip); it counts them, the block scans the counts into slice bases,
+// then each wave places its slice in order, 64 pairs at a time.
 constexpr int kFusedWaves = 16;
-constexpr int kFusedPairs = kFusedWaves * 512;
+constexpr int kFusedMaxPPL = 4;
+constexpr int kFusedPairs = kFusedWaves * 64 * kFusedMaxPPL;
 constexpr int kFusedExperts = 256;
 
+template <int PPL>
 __device__ void permute_block(
     const int32_t *idx, int64_t T, int k, int E, int n_shared, int bm, int max_tiles, int key_bits,
     int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *row_pair, int32_t *inv_perm,
@@ -233,20 +240,23 @@ __device__ void permute_block(
   __shared__ int sh[17];
   __shared__ int s_off[kFusedExperts + 8];
   const int w = threadIdx.x >> 6, lane = lane_id();
-  const int64_t P = T * k;
-  const int slice = int((P + kFusedWaves * 64 - 1) / (kFusedWaves * 64)) * 64;
+  const int P = int(T) * k;  // <= kFusedPairs
+  const int Ti = int(T);
   for (int i = threadIdx.x; i < kFusedWaves * kFusedExperts; i += blockDim.x) (&cnt[0][0])[i] = 0;
-  __syncthreads();
-  const int64_t p0 = int64_t(w) * slice;
-  for (int it = 0; it < slice; it += 64) {
-    const int64_t p = p0 + it + lane;
-    if (p < P) {
-      int64_t t;
-      int sl;
-      const int e = pair_expert(idx, p, T, k, &t, &sl);
-      if (e >= 0 && e < E) atomicAdd(&cnt[w][e], 1);
-    }
+  // expert of pair p = slot * T + t (-1: past the end or an id outside 0..E-1)
+  int ex[PPL];
+  const int p0 = w * 64 * PPL + lane;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int p = p0 + 64 * j;
+    const int sl = p / Ti, t = p - sl * Ti;
+    const int e = p < P ? idx[int64_t(t) * k + sl] : -1;
+    ex[j] = (e >= 0 && e < E) ? e : -1;
   }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PPL; ++j)
+    if (ex[j] >= 0) atomicAdd(&cnt[w][ex[j]], 1);
   __syncthreads();
   const int e = threadIdx.x;
   int c = 0;
@@ -266,38 +276,141 @@ __device__ void permute_block(
     }
   }
   __syncthreads();
-  for (int it = 0; it < slice; it += 64) {
-    const int64_t p = p0 + it + lane;
-    bool valid = p < P;
-    int64_t t = 0;
-    int sl = 0, ex = 0;
-    if (valid) {
-      ex = pair_expert(idx, p, T, k, &t, &sl);
-      valid = ex >= 0 && ex < E;
-      if (!valid) ex = 0;
-    }
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const bool valid = ex[j] >= 0;
+    const int exj = valid ? ex[j] : 0;
     int rank, group;
     bool leader;
-    peer_rank(valid, ex, key_bits, &rank, &group, &leader);
-    const int start = valid ? cnt[w][ex] : 0;
+    peer_rank(valid, exj, key_bits, &rank, &group, &leader);
+    const int start = valid ? cnt[w][exj] : 0;
     __builtin_amdgcn_wave_barrier();
-    if (leader) cnt[w][ex] = start + group;
+    if (leader) cnt[w][exj] = start + group;
     __builtin_amdgcn_wave_barrier();
     if (valid) {
+      const int p = p0 + 64 * j;
+      const int sl = p / Ti, t = p - sl * Ti;
       const int pos = start + rank;
-      const int pair = int(t * k + sl);
+      const int pair = t * k + sl;
       row_pair[pos] = pair;
-      row_token[pos] = int32_t(t);
+      row_token[pos] = t;
       inv_perm[pair] = pos;
     }
   }
 }
 
+// Mid-size batches (kFusedPairs < T * k <= kChunkedPairs, E + n_shared <=
+// 256): two launches of one 256-thread work-group per kWgChunk positions.
+// The first counts each chunk's experts; the second has every work-group sum
+// the chunk counts itself (totals, and the prefix over earlier chunks), so no
+// separate scan launch is needed, and place its chunk in order.  Work-group
+// 0 also writes counts, offsets, the tile schedule and the shared rows.
+constexpr int kWgChunk = 512;
+constexpr int kChunkedPairs = 65536;
+
+__global__ __launch_bounds__(256) void chunk_hist_kernel(const int32_t *idx, int64_t T, int k, int E,
+                                                         int32_t *cc) {
+  __shared__ int cnt[kFusedExperts];
+  const int c = blockIdx.x, Ti = int(T), P = int(T) * k;
+  for (int i = threadIdx.x; i < E; i += 256) cnt[i] = 0;
+  int ex[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = c * kWgChunk + 256 * j + threadIdx.x;
+    const int sl = p / Ti, t = p - sl * Ti;
+    const int e = p < P ? idx[int64_t(t) * k + sl] : -1;
+    ex[j] = (e >= 0 && e < E) ? e : -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (ex[j] >= 0) atomicAdd(&cnt[ex[j]], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) cc[int64_t(c) * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(256) void chunk_scatter_kernel(
+    const int32_t *idx, int64_t T, int k, int E, int n_shared, int bm, int max_tiles, int key_bits,
+    int nchunks, const int32_t *cc, int32_t *counts, int32_t *offsets, int32_t *row_token,
+    int32_t *row_pair, int32_t *inv_perm, int32_t *tiles, int32_t *n_tiles) {
+  __shared__ int sh[17];
+  __shared__ int s_off[kFusedExperts + 8];
+  __shared__ int wcnt[4][kFusedExperts];
+  const int c = blockIdx.x, e = threadIdx.x, w = e >> 6, lane = lane_id();
+  const int Ti = int(T), P = int(T) * k;
+  // this expert's rows over all chunks, and over the chunks before this one
+  int tot = 0, pre = 0;
+  if (e < E) {
+    for (int ch = 0; ch < nchunks; ++ch) {
+      const int v = cc[int64_t(ch) * E + e];
+      tot += v;
+      pre += ch < c ? v : 0;
+    }
+  } else if (e < E + n_shared) {
+    tot = Ti;
+  }
+  // the expert's first row (schedule() also writes the outputs; one block does)
+  int off;
+  if (c == 0) {
+    off = schedule(tot, E, n_shared, T, bm, max_tiles, counts, offsets, row_token, tiles, n_tiles, sh, s_off);
+  } else {
+    int total;
+    off = block_exclusive_scan(e < E + n_shared ? tot : 0, sh, &total);
+  }
+  // this chunk's pairs: wave w takes positions [128 w, 128 w + 128) of it
+  int ex[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = c * kWgChunk + 128 * w + 64 * j + lane;
+    const int sl = p / Ti, t = p - sl * Ti;
+    const int v = p < P ? idx[int64_t(t) * k + sl] : -1;
+    ex[j] = (v >= 0 && v < E) ? v : -1;
+  }
+  for (int i = threadIdx.x; i < 4 * kFusedExperts; i += 256) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (ex[j] >= 0) atomicAdd(&wcnt[w][ex[j]], 1);
+  __syncthreads();
+  if (e < E) {
+    int run = off + pre;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const int v = wcnt[ww][e];
+      wcnt[ww][e] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const bool valid = ex[j] >= 0;
+    const int exj = valid ? ex[j] : 0;
+    int rank, group;
+    bool leader;
+    peer_rank(valid, exj, key_bits, &rank, &group, &leader);
+    const int start = valid ? wcnt[w][exj] : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (leader) wcnt[w][exj] = start + group;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      const int p = c * kWgChunk + 128 * w + 64 * j + lane;
+      const int sl = p / Ti, t = p - sl * Ti;
+      const int pos = start + rank;
+      const int pair = t * k + sl;
+      row_pair[pos] = pair;
+      row_token[pos] = t;
+      inv_perm[pair] = pos;
+    }
+  }
+}
+
+template <int PPL>
 __global__ __launch_bounds__(1024) void permute_fused_kernel(
     const int32_t *idx, int64_t T, int k, int E, int n_shared, int bm, int max_tiles, int key_bits,
     int32_t *counts, int32_t *offsets, int32_t *row_token, int32_t *row_pair, int32_t *inv_perm,
     int32_t *tiles, int32_t *n_tiles) {
-  permute_block(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
+  permute_block<PPL>(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
                 inv_perm, tiles, n_tiles);
 }
 
@@ -305,7 +418,7 @@ __global__ __launch_bounds__(1024) void permute_fused_kernel(
 // the selection by the same work-group: one launch instead of two for small
 // batches.  The selected indices are read back after the barrier, which
 // makes the waves' global stores visible to the whole work-group.
-template <int EREG>
+template <int EREG, int PPL>
 __global__ __launch_bounds__(1024) void topk_permute_kernel(
     const void *logits, int dtype, int64_t T, int E, int k, int norm, int32_t *idx, float *w,
     int n_shared, int bm, int max_tiles, int key_bits, int32_t *counts, int32_t *offsets,
@@ -321,9 +434,12 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
     select_topk<EREG>(vals, E, k, norm, t, idx, w);
   }
   __syncthreads();
-  permute_block(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
-                inv_perm, tiles, n_tiles);
+  permute_block<PPL>(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
+                     inv_perm, tiles, n_tiles);
 }
+
+// Pairs per lane of the single-work-group permutation for P <= kFusedPairs.
+static int fused_ppl(int64_t P) { return P <= kFusedWaves * 64 ? 1 : 4; }
 
 bool topk_permute_fits(int64_t T, int k, int E, int n_shared) {
   return T * k <= kFusedPairs && E + n_shared <= kFusedExperts && k <= kMaxTopK;
@@ -342,14 +458,15 @@ int launch_topk_permute(const void *logits, int dtype, int64_t T, int E, int k, 
   if (!topk_permute_fits(T, k, E, n_shared)) return fail(MOEQ_ERR_UNSUPPORTED, "topk_permute: batch too large");
   const int max_tiles = moeq_max_tiles(T, k, E, n_shared, bm);
   const int kb = key_bits_for(E);
-#define MOEQ_TP(R)                                                                                      \
-  topk_permute_kernel<R><<<1, 1024, 0, s>>>(logits, dtype, T, E, k, norm, idx, w, n_shared, bm, max_tiles, \
-                                            kb, counts, offsets, row_token, row_pair, inv_perm, tiles,   \
-                                            n_tiles)
+#define MOEQ_TP(R, Q)                                                                                       \
+  topk_permute_kernel<R, Q><<<1, 1024, 0, s>>>(logits, dtype, T, E, k, norm, idx, w, n_shared, bm,          \
+                                               max_tiles, kb, counts, offsets, row_token, row_pair, inv_perm, \
+                                               tiles, n_tiles)
+  const bool one = fused_ppl(T * k) == 1;
   switch (ereg_for(E)) {
-    case 1: MOEQ_TP(1); break;
-    case 2: MOEQ_TP(2); break;
-    default: MOEQ_TP(4); break;  // E <= kFusedExperts = 256
+    case 1: if (one) MOEQ_TP(1, 1); else MOEQ_TP(1, 4); break;
+    case 2: if (one) MOEQ_TP(2, 1); else MOEQ_TP(2, 4); break;
+    default: if (one) MOEQ_TP(4, 1); else MOEQ_TP(4, 4); break;  // E <= kFusedExperts = 256
   }
 #undef MOEQ_TP
   return check_launch("route/topk_permute");
@@ -396,9 +513,22 @@ extern "C" int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
   const int key_bits = key_bits_for(E);
   hipStream_t s = as_stream(stream);
   const int max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm);
+  if (T * top_k > kFusedPairs && T * top_k <= kChunkedPairs && E + n_shared <= kFusedExperts) {
+    int32_t *cc = static_cast<int32_t *>(ws);
+    const int nchunks = int(cdiv(T * top_k, kWgChunk));
+    chunk_hist_kernel<<<nchunks, 256, 0, s>>>(idx, T, top_k, E, cc);
+    int rc = check_launch("permute/chunk_hist");
+    if (rc) return rc;
+    chunk_scatter_kernel<<<nchunks, 256, 0, s>>>(idx, T, top_k, E, n_shared, bm, max_tiles, key_bits, nchunks, cc,
+                                                 counts, offsets, row_token, row_pair, inv_perm, tiles, n_tiles);
+    return check_launch("permute/chunk_scatter");
+  }
   if (T * top_k <= kFusedPairs && E + n_shared <= kFusedExperts) {
-    permute_fused_kernel<<<1, 1024, 0, s>>>(idx, T, top_k, E, n_shared, bm, max_tiles, key_bits, counts,
-                                            offsets, row_token, row_pair, inv_perm, tiles, n_tiles);
+#define MOEQ_PF(Q)                                                                                       \
+  permute_fused_kernel<Q><<<1, 1024, 0, s>>>(idx, T, top_k, E, n_shared, bm, max_tiles, key_bits, counts, \
+                                             offsets, row_token, row_pair, inv_perm, tiles, n_tiles)
+    if (fused_ppl(T * top_k) == 1) MOEQ_PF(1); else MOEQ_PF(4);
+#undef MOEQ_PF
     return check_launch("permute/fused");
   }
   int32_t *cc = static_cast<int32_t *>(ws);

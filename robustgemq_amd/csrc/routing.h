@@ -211,8 +211,8 @@ int launch_route_logits(const RouteArgs &a, hipStream_t s);
 bool launch_logits_topk(const RouteArgs &a, hipStream_t s);
 
 // Top-k of T rows of logits followed by the token -> expert permutation, in
-// one work-group; valid when T * k <= kFusedPairs and E + n_shared <=
-// kFusedExperts (permute.hip).
+// one work-group; valid when T * k <= 4096, E + n_shared <= 256 and
+// k <= kMaxTopK (permute.hip).
 int launch_topk_permute(const void *logits, int dtype, int64_t T, int E, int k, int norm, int32_t *idx,
                         float *w, int n_shared, int bm, int32_t *counts, int32_t *offsets,
                         int32_t *row_token, int32_t *row_pair, int32_t *inv_perm, int32_t *tiles,
