@@ -68,6 +68,24 @@ def time_events(fn, steps, warmup, stream):
     return t0.elapsed_time(t1) / steps  # ms
 
 
+def time_graph(fn, steps, warmup, stream):
+    """Device time of a short stage: fn is captured once in a CUDA graph and
+    the graph replayed, so the Python and ctypes cost of each call (larger
+    than a few-microsecond kernel) is not in the measurement."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(stream)
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    stream.wait_stream(s)
+    torch.cuda.synchronize()
+    return time_events(g.replay, steps, warmup, stream)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -150,7 +168,8 @@ def main():
     kt = {}
     for name, fn in (("route", route_only), ("permute", permute_only), ("gate_up", gate_up), ("down", down),
                      ("combine", combine_only)):
-        kt[name] = time_events(fn, args.steps, 3, stream)
+        timer = time_events if name in ("gate_up", "down") else time_graph
+        kt[name] = timer(fn, args.steps, 3, stream)
     gu_flops = 2.0 * rows * 2 * cfg.hidden * cfg.inter
     dn_flops = 2.0 * rows * cfg.hidden * cfg.inter
     gu_tflops = gu_flops / (kt["gate_up"] * 1e-3) / 1e12
