@@ -56,6 +56,9 @@ CONFIGS = {
     "mixtral_mixed": LayerConfig("mixtral_mixed", "mixtral", 4096, 14336, 8, 2, True, 64,
                                  ("mix", {2: 4, 3: 2, 4: 2}), torch.bfloat16,
                                  runs={"decode": (1, 16, 64), "prefill": (1024,)}),
+    # Mixtral family at a test-sized shape (always-renormalised top-2, bf16)
+    "mixtral_small": LayerConfig("mixtral_small", "mixtral", 1024, 3584, 8, 2, True, 64,
+                                 ("mix", {2: 4, 3: 2, 4: 2}), torch.bfloat16, runs={"prefill": (300,)}),
     # the reference's own block-test shape (tests/test_moe_block_equiv.py:29-38)
     "ref_test": LayerConfig("ref_test", "olmoe", 512, 512, 8, 2, False, 128,
                             ("list", (1, 2, 3, 2, 3, 1, 2, 3)), torch.float16, runs={"prefill": (16,)}),

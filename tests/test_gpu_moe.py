@@ -114,6 +114,15 @@ def test_layer_matches_oracle_qwen3_bf16(device, T):
     _check(cfg, block, w, dense, T)
 
 
+@pytest.mark.parametrize("T", [1, 16, 64, 300])
+def test_layer_matches_oracle_mixtral_bf16(device, T):
+    """Mixtral family: top-2 always renormalised (moe_block.py:245-249), w1/w3/w2
+    naming, bf16 activations, a down projection with K = 3584."""
+    _say(f"[layer] mixtral_small T={T}")
+    cfg, w, block, dense = _layer("mixtral_small")
+    _check(cfg, block, w, dense, T)
+
+
 @pytest.mark.parametrize("T", [1, 300])
 def test_layer_matches_oracle_deepseek_shared_zipf(device, T):
     _say(f"[layer] deepseek_v2_lite T={T}")
