@@ -237,7 +237,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
     const int cfirst = KS ? c0 + wave : c0, cstep = KS ? NW : 1;
     const int nc = KS ? (c1 > c0 + wave ? (c1 - c0 - wave + NW - 1) / NW : 0) : max(c1 - c0, 0);
     auto fetch = [&](int j, uint4 (&av)[4], uint32_t (&w)[NP][NB][BITS], uint32_t (&sz)[NP][NB]) {
-      const int c = cfirst + cstep * min(j, max(nc - 1, 0));
+      // a K-split wave with no chunk of its own (fewer chunks than waves, or
+      // an empty split) still fetches a valid chunk, c1 - 1, times zero
+      const int c = max(min(cfirst + cstep * min(j, max(nc - 1, 0)), c1 - 1), 0);
       const uint4 *pa = reinterpret_cast<const uint4 *>(arow + (int64_t(c) * 128 + 32 * kb) * AES);
 #pragma unroll
       for (int t = 0; t < 4; ++t) av[t] = pa[t];
