@@ -139,6 +139,35 @@ __device__ void logit_tile(const RouteArgs &a, int64_t t0, int e0) {
   for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
     for (int ee = 0; ee < EE; ++ee) ch[tt][ee] = 0.f;
+  if constexpr (TT == 1 && EE == 1) {
+    // one logit per wave (decode): every k step's loads are issued before
+    // the first multiply-add, so the wave waits for memory once.  Lanes past
+    // H load the row's last 8 values and skip the multiply-adds.
+    const int64_t xr = min(t0, a.T - 1) * a.H;
+    const int64_t wr = int64_t(min(e0, a.E - 1)) * a.H;
+    float xv[MAXCH][8], wv[MAXCH][8];
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+      const int kc = min(512 * i + 8 * lane, a.H - 8);
+      load8(a.x, a.x_dtype, xr + kc, xv[i]);
+      load8(a.wg, a.wg_dtype, wr + kc, wv[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+      const int k0 = 512 * i + 8 * lane;
+      if (k0 < a.H) {
+        if (a.x16 && e0 == 0) {  // the activations the expert GEMMs read, converted once
+          uint32_t h[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            h[j] = uint32_t(f32_to_f16_bits(xv[i][2 * j])) | (uint32_t(f32_to_f16_bits(xv[i][2 * j + 1])) << 16);
+          *reinterpret_cast<uint4 *>(a.x16 + t0 * a.H + k0) = (uint4){h[0], h[1], h[2], h[3]};
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ch[0][0] = __builtin_fmaf(xv[i][j], wv[i][j], ch[0][0]);
+      }
+    }
+  } else
 #pragma unroll
   for (int i = 0; i < MAXCH; ++i) {
     const int k0 = 512 * i + 8 * lane;
