@@ -341,7 +341,20 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
   // this expert's rows over all chunks, and over the chunks before this one
   int tot = 0, pre = 0;
   if (e < E) {
-    for (int ch = 0; ch < nchunks; ++ch) {
+    // eight chunk counts in flight per trip (up to 128 chunks: one serial
+    // load round trip per chunk would dominate the launch)
+    int ch = 0;
+    for (; ch + 8 <= nchunks; ch += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = cc[int64_t(ch + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        tot += v[u];
+        pre += ch + u < c ? v[u] : 0;
+      }
+    }
+    for (; ch < nchunks; ++ch) {
       const int v = cc[int64_t(ch) * E + e];
       tot += v;
       pre += ch < c ? v : 0;

@@ -11,7 +11,7 @@ namespace moeq {
 
 template <int TT, int EE, int MAXCH>
 __global__ __launch_bounds__(256) void logits_kernel(RouteArgs a, int n_et) {
-  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t wave = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   logit_tile<TT, EE, MAXCH>(a, (wave / n_et) * TT, int(wave % n_et) * EE);
 }
 
@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256) void topk_from_logits_kernel(
     const void *logits, int dtype, int64_t T, int E, int k, int norm,
     int32_t *idx, float *w) {
   const int lane = lane_id();
-  const int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t t = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= T) return;
   float vals[EREG];
 #pragma unroll
@@ -109,12 +109,17 @@ __device__ __forceinline__ float halving_sum(float (&c)[64]) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[j]), __float_as_uint(a[j + 16]), false, false);
     a[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
+  // Levels 8 .. 1: the lane picks with an explicit v_cndmask on its own two
+  // registers (a plain `up ? a[j] : a[j + o]` is folded by the compiler into
+  // a lane-dependent index into a[], lowered as a 32-way select chain).
 #pragma unroll
   for (int o = 8; o >= 1; o >>= 1) {
-    const bool up = lane & o;
+    const uint64_t up = __builtin_amdgcn_ballot_w64((lane & o) != 0);
 #pragma unroll
     for (int j = 0; j < o; ++j) {
-      const float send = up ? a[j] : a[j + o], keep = up ? a[j + o] : a[j];
+      float send, keep;
+      asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(send) : "v"(a[j + o]), "v"(a[j]), "s"(up));
+      asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(keep) : "v"(a[j]), "v"(a[j + o]), "s"(up));
       a[j] = keep + __shfl_xor(send, o);
     }
   }
@@ -125,7 +130,7 @@ template <int XDT, int WDT, int NWV, int MAXCH>
 __global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
   __shared__ float lg[kTT][512];
   const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t0 = int64_t(blockIdx.x) * kTT;
   const int n_eb = (a.E + kEE - 1) / kEE;
   // two k steps in flight for fp16 rows; widened operands need the registers
