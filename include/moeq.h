@@ -234,6 +234,13 @@ int moeq_gemm_tile_n(int bm, int epilogue);
  * max_tiles, dtype of the grouped down-projection output}. */
 int moeq_moe_plan(const moeq_moe *m, int64_t T, int32_t *out4);
 
+/* Byte offsets, in the workspace of moeq_moe_forward for T tokens, of the
+ * routing and permutation it leaves there: out9 = {idx, w, counts, offsets,
+ * row_token, row_pair, inv_perm, tiles, n_tiles} (layouts as moeq_route and
+ * moeq_permute write them).  Introspection for tests; no reference
+ * counterpart. */
+int moeq_moe_workspace_layout(const moeq_moe *m, int64_t T, int64_t *out9);
+
 #ifdef __cplusplus
 }
 #endif

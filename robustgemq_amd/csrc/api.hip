@@ -163,10 +163,19 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
                  m->act_dtype == MOEQ_BF16 ? static_cast<uint16_t *>(at(p.off_x16)) : nullptr};
     x16_done = m->act_dtype == MOEQ_BF16;
     hipStream_t s = as_stream(stream);
-    if ((rc = launch_route_logits(ra, s))) return rc;
-    rc = launch_topk_permute(lg, lg_dt, T, m->n_experts, m->top_k, m->norm_topk ? 1 : 0, idx, w, m->n_shared,
-                             p.bm, counts, offsets, row_token, row_pair, inv, tiles, n_tiles, s);
-    if (rc) return rc;
+    // one token: logits, top-k and the (trivial) grouping in one launch
+    const PermOut po{m->n_shared, p.max_tiles, counts, offsets, row_token, row_pair, inv, tiles, n_tiles};
+    RouteArgs r1 = ra;  // its logits stay in LDS unless asked for
+    r1.logits = logits_out;
+    r1.store_dtype = ldt;
+    if (launch_route1(r1, po, s)) {
+      if ((rc = check_launch("moe/route1"))) return rc;
+    } else {
+      if ((rc = launch_route_logits(ra, s))) return rc;
+      rc = launch_topk_permute(lg, lg_dt, T, m->n_experts, m->top_k, m->norm_topk ? 1 : 0, idx, w, m->n_shared,
+                               p.bm, counts, offsets, row_token, row_pair, inv, tiles, n_tiles, s);
+      if (rc) return rc;
+    }
   } else {
     // larger batches: fused logits + top-k (writing the fp16 copy of bf16
     // activations on the way) where it covers the dtypes, else moeq_route
@@ -236,6 +245,21 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
 
   return moeq_combine(at(p.off_y), p.y_dtype, p.splits, p.rows * m->hidden, m->hidden, inv, w, T,
                       m->top_k, m->n_shared, m->hidden, out, out_dtype, stream);
+}
+
+// Workspace introspection for tests (not a reference interface): byte
+// offsets in the forward's workspace of {idx, w, counts, offsets, row_token,
+// row_pair, inv_perm, tiles, n_tiles}, the routing and permutation the
+// forward leaves there.
+extern "C" int moeq_moe_workspace_layout(const moeq_moe *m, int64_t T, int64_t *out9) {
+  int rc = check_layer(m);
+  if (rc) return rc;
+  if (T <= 0 || !out9) return fail(MOEQ_ERR_INVALID, "moe_workspace_layout: T=%lld", (long long)T);
+  const Plan p = make_plan(m, T);
+  const size_t offs[9] = {p.off_idx, p.off_w, p.off_counts, p.off_offsets, p.off_row_token,
+                          p.off_row_pair, p.off_inv, p.off_tiles, p.off_ntiles};
+  for (int i = 0; i < 9; ++i) out9[i] = int64_t(offs[i]);
+  return MOEQ_OK;
 }
 
 // Launch plan introspection for tests and the benchmark (not a reference

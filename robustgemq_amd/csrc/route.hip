@@ -5,6 +5,9 @@
 // The xor butterfly (o = 32 .. 1, v <- v + v[l ^ o]) gives every lane the
 // same value because fp32 addition is commutative.  oracle/router_exact.c
 // replays exactly this order, so routing is bit-reproducible on the CPU.
+#include <algorithm>
+#include <type_traits>
+
 #include "routing.h"
 
 namespace moeq {
@@ -260,6 +263,170 @@ static void launch_logits_topk_dt(const RouteArgs &a, int maxch, hipStream_t s) 
   else if (a.E <= 16) launch_logits_topk_nw<XDT, WDT, 2>(a, maxch, s);
   else if (a.E <= 32) launch_logits_topk_nw<XDT, WDT, 4>(a, maxch, s);
   else launch_logits_topk_nw<XDT, WDT, 8>(a, maxch, s);
+}
+
+// ---------------------------------------------------------------- one token
+// Eight waves; wave w computes the logits of experts w * EE .. w * EE + EE - 1,
+// then (w + 8) * EE .., with every k step of the x row and of its EE gate
+// rows loaded at once (one memory round trip per expert group).  Each logit
+// is the same chain and butterfly as logit_tile's.  The rounded logits meet
+// in LDS; wave 0 ranks them and writes idx / w and the permutation.
+constexpr int kR1Waves = 8;
+
+template <int XDT, int WDT, int EE, int MAXCH>
+__global__ __launch_bounds__(kR1Waves * 64) void route1_kernel(RouteArgs a, PermOut po) {
+  __shared__ float lg[256];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr uint32_t XES = XDT == MOEQ_F32 ? 4 : 2, WES = WDT == MOEQ_F32 ? 4 : 2;
+  // k steps past H load the row's last 8 values and skip the multiply-adds
+  uint32_t kc[MAXCH];
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) kc[i] = uint32_t(min(512 * i + 8 * lane, a.H - 8));
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), (short)0, 0x7fffffff, 0x00020000);
+  Raw8<XDT> xb[MAXCH];
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) xb[i].load(xrs, kc[i] * XES, 0);
+  for (int e0 = wave * EE; e0 < a.E; e0 += kR1Waves * EE) {
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char *>(static_cast<const char *>(a.wg) + int64_t(e0) * a.H * WES), (short)0, 0x7fffffff,
+        0x00020000);
+    Raw8<WDT> wb[MAXCH][EE];
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i)
+#pragma unroll
+      for (int ee = 0; ee < EE; ++ee)
+        wb[i][ee].load(wrs, kc[i] * WES, uint32_t(min(ee, a.E - 1 - e0)) * uint32_t(a.H) * WES);
+    if (a.x16 && e0 == 0) {  // the activations the expert GEMMs read, converted once
+#pragma unroll
+      for (int i = 0; i < MAXCH; ++i) {
+        const int k0 = 512 * i + 8 * lane;
+        if (k0 < a.H) {
+          uint32_t h[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            h[j] = uint32_t(f32_to_f16_bits(xb[i].value(2 * j))) |
+                   (uint32_t(f32_to_f16_bits(xb[i].value(2 * j + 1))) << 16);
+          *reinterpret_cast<uint4 *>(a.x16 + k0) = (uint4){h[0], h[1], h[2], h[3]};
+        }
+      }
+    }
+    float ch[EE];
+#pragma unroll
+    for (int ee = 0; ee < EE; ++ee) ch[ee] = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+      if (512 * i + 8 * lane < a.H) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xv = xb[i].value(j);
+#pragma unroll
+          for (int ee = 0; ee < EE; ++ee) ch[ee] = __builtin_fmaf(xv, wb[i][ee].value(j), ch[ee]);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+      for (int ee = 0; ee < EE; ++ee) ch[ee] = ch[ee] + __shfl_xor(ch[ee], o);
+#pragma unroll
+    for (int ee = 0; ee < EE; ++ee) {
+      const int e = e0 + ee;
+      if (e < a.E) {
+        float v = ch[ee];
+        if (a.bias) v = v + a.bias[e];
+        v = round_logit(v, a.logits_dtype);
+        if (lane == 0) lg[e] = v;
+        if (a.logits && lane == ee) store_logit(a.logits, a.store_dtype, e, v);
+      }
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int E = a.E, k = a.k;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  auto finish = [&](auto regs) {
+    constexpr int R = decltype(regs)::value;
+    float vals[R];
+    int rank[R];
+    float wsel[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) vals[r] = 64 * r + lane < E ? lg[64 * r + lane] : -INFINITY;
+    topk_ranks<R>(vals, E, k, a.norm, rank, wsel);
+    int before = 0;  // selected experts in earlier registers
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int e = 64 * r + lane;
+      const bool sel = e < E && rank[r] < k;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(sel);
+      const int pos = before + __popcll(m & lt);  // row = selected experts below e
+      if (e < E) {
+        po.counts[e] = sel ? 1 : 0;
+        po.offsets[e] = pos;
+      }
+      if (sel) {
+        a.idx[rank[r]] = e;
+        a.w[rank[r]] = wsel[r];
+        po.row_pair[pos] = rank[r];
+        po.row_token[pos] = 0;
+        po.inv_perm[rank[r]] = pos;
+        *reinterpret_cast<int4 *>(po.tiles + 4 * pos) = (int4){e, pos, 1, 0};
+      }
+      before += __popcll(m);
+    }
+  };
+  const int ereg = ereg_for(E);
+  if (ereg == 1) finish(std::integral_constant<int, 1>{});
+  else if (ereg == 2) finish(std::integral_constant<int, 2>{});
+  else finish(std::integral_constant<int, 4>{});
+  // shared experts: one row each after the k routed rows
+  for (int v = lane; v < po.n_shared; v += 64) {
+    po.counts[E + v] = 1;
+    po.offsets[E + v] = k + v;
+    po.row_token[k + v] = 0;
+    *reinterpret_cast<int4 *>(po.tiles + 4 * (k + v)) = (int4){E + v, k + v, 1, 0};
+  }
+  if (lane == 0) {
+    po.offsets[E + po.n_shared] = k + po.n_shared;
+    *po.n_tiles = min(k + po.n_shared, po.max_tiles);
+  }
+}
+
+// Expert group per wave: no larger than the experts need over 8 waves, and
+// no larger than FIT, the largest group whose loaded rows stay in registers
+// (16-bit gate rows: 8 at H <= 2048, 4 above; fp32 rows: 4 and 1).
+template <int WDT, int MAXCH>
+constexpr int route1_fit() {
+  return WDT == MOEQ_F32 ? (MAXCH <= 4 ? 4 : 1) : (MAXCH <= 4 ? 8 : 4);
+}
+
+template <int XDT, int WDT, int MAXCH>
+static void launch_route1_ch(const RouteArgs &a, const PermOut &po, hipStream_t s) {
+  constexpr int FIT = route1_fit<WDT, MAXCH>();
+  int ee = 1;
+  while (ee < FIT && ee * kR1Waves < a.E) ee <<= 1;
+  if (ee == 1) route1_kernel<XDT, WDT, 1, MAXCH><<<1, kR1Waves * 64, 0, s>>>(a, po);
+  if constexpr (FIT >= 2) if (ee == 2) route1_kernel<XDT, WDT, 2, MAXCH><<<1, kR1Waves * 64, 0, s>>>(a, po);
+  if constexpr (FIT >= 4) if (ee == 4) route1_kernel<XDT, WDT, 4, MAXCH><<<1, kR1Waves * 64, 0, s>>>(a, po);
+  if constexpr (FIT >= 8) if (ee == 8) route1_kernel<XDT, WDT, 8, MAXCH><<<1, kR1Waves * 64, 0, s>>>(a, po);
+}
+
+template <int XDT, int WDT>
+static void launch_route1_dt(const RouteArgs &a, const PermOut &po, hipStream_t s) {
+  if (a.H <= 2048) launch_route1_ch<XDT, WDT, 4>(a, po, s);
+  else launch_route1_ch<XDT, WDT, 8>(a, po, s);
+}
+
+bool launch_route1(const RouteArgs &a, const PermOut &po, hipStream_t s) {
+  if (a.T != 1 || a.E > 256 || a.k > kMaxTopK || a.k > a.E || a.H % 8 || a.H > 4096) return false;
+  const int x = a.x_dtype, w = a.wg_dtype;
+  if (x == MOEQ_F16 && w == MOEQ_F16) launch_route1_dt<MOEQ_F16, MOEQ_F16>(a, po, s);
+  else if (x == MOEQ_F16 && w == MOEQ_F32) launch_route1_dt<MOEQ_F16, MOEQ_F32>(a, po, s);
+  else if (x == MOEQ_BF16 && w == MOEQ_BF16) launch_route1_dt<MOEQ_BF16, MOEQ_BF16>(a, po, s);
+  else if (x == MOEQ_BF16 && w == MOEQ_F32) launch_route1_dt<MOEQ_BF16, MOEQ_F32>(a, po, s);
+  else return false;
+  return true;
 }
 
 // Fused logits + top-k for batches above T * E = 16384; returns false (and

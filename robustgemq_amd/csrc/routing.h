@@ -69,19 +69,20 @@ __device__ __forceinline__ void load8(const void *p, int dtype, int64_t i, float
 // Top-k of the logits held by one wave (expert e = 64 r + lane in vals[r]),
 // ranked by value with ties to the lower index (NaN ranks last); softmax
 // weights over all E experts; optional renormalisation over the selected k.
-// Writes row t.  Each expert's rank is counted directly: every value is
-// broadcast once (v_readlane) and compared with all of them, so there is no
-// sequential select-and-remove loop and no dynamically indexed register.
+// topk_ranks leaves each expert's rank and routing weight in the lane that
+// holds it; select_topk writes row t.  Each expert's rank is counted
+// directly: every value is broadcast once (v_readlane) and compared with all
+// of them, so there is no sequential select-and-remove loop and no
+// dynamically indexed register.
 template <int EREG>
-__device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
-                            int64_t t, int32_t *idx_out, float *w_out) {
+__device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&rank)[EREG],
+                           float (&wsel)[EREG]) {
   const int lane = lane_id();
 #pragma unroll
   for (int r = 0; r < EREG; ++r) {
     const int e = 64 * r + lane;
     if (e >= E || vals[r] != vals[r]) vals[r] = -INFINITY;  // NaN ranks last
   }
-  int rank[EREG];
 #pragma unroll
   for (int r = 0; r < EREG; ++r) rank[r] = 0;
   float m = -INFINITY;
@@ -117,11 +118,22 @@ __device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) psum += __shfl_xor(psum, o);
 #pragma unroll
+  for (int r = 0; r < EREG; ++r) wsel[r] = norm ? p[r] / psum : p[r];
+}
+
+template <int EREG>
+__device__ void select_topk(float (&vals)[EREG], int E, int k, int norm,
+                            int64_t t, int32_t *idx_out, float *w_out) {
+  const int lane = lane_id();
+  int rank[EREG];
+  float wsel[EREG];
+  topk_ranks<EREG>(vals, E, k, norm, rank, wsel);
+#pragma unroll
   for (int r = 0; r < EREG; ++r) {
     const int e = 64 * r + lane;
     if (e < E && rank[r] < k) {
       idx_out[t * k + rank[r]] = e;
-      w_out[t * k + rank[r]] = norm ? p[r] / psum : p[r];
+      w_out[t * k + rank[r]] = wsel[r];
     }
   }
 }
@@ -247,5 +259,20 @@ int launch_topk_permute(const void *logits, int dtype, int64_t T, int E, int k, 
                         int32_t *row_token, int32_t *row_pair, int32_t *inv_perm, int32_t *tiles,
                         int32_t *n_tiles, hipStream_t s);
 bool topk_permute_fits(int64_t T, int k, int E, int n_shared);
+
+// Outputs of the token -> expert permutation (moeq_permute's arrays).
+struct PermOut {
+  int n_shared, max_tiles;
+  int32_t *counts, *offsets, *row_token, *row_pair, *inv_perm, *tiles, *n_tiles;
+};
+
+// One token (decode): logits, top-k and the permutation in one work-group.
+// With a single token every selected expert holds one row, so the stable
+// grouping is the selected experts in id order, one 1-row tile each, then
+// the shared experts' rows: exactly moeq_permute's output for T = 1.  Needs
+// T == 1, E <= 256, k <= kMaxTopK, H % 8 == 0, H <= 4096 and the dtype pairs
+// (x, gate) f16/f16, f16/f32, bf16/bf16, bf16/f32; returns false without
+// launching otherwise (route.hip).
+bool launch_route1(const RouteArgs &a, const PermOut &po, hipStream_t s);
 
 }  // namespace moeq

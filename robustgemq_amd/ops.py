@@ -156,6 +156,14 @@ class MoELayer:
         L.check(L.lib().moeq_moe_plan(self.desc, T, buf), "moeq_moe_plan")
         return dict(bm=buf[0], splits=buf[1], max_tiles=buf[2], y_dtype=buf[3])
 
+    def workspace_layout(self, T):
+        """Byte offsets in the forward's workspace of idx, w, counts, offsets,
+        row_token, row_pair, inv_perm, tiles, n_tiles (for tests)."""
+        import ctypes
+        buf = (ctypes.c_int64 * 9)()
+        L.check(L.lib().moeq_moe_workspace_layout(self.desc, T, buf), "moeq_moe_workspace_layout")
+        return list(buf)
+
     def workspace(self, T, device):
         need = max(self.workspace_size(T), 1)
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:

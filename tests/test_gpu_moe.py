@@ -132,6 +132,48 @@ def test_layer_matches_oracle_deepseek_shared_zipf(device, T):
     _check(cfg, block, w, dense, T)
 
 
+@pytest.mark.parametrize("name", ["ref_test", "olmoe_mixed", "qwen3_mixed", "mixtral_small", "deepseek_v2_lite"])
+def test_one_token_forward_routing(device, name):
+    """A one-token forward routes and groups in a single launch; the logits it
+    returns and the selection, weights and permutation it leaves in its
+    workspace equal the oracle's (and moeq_route's weights) bit for bit, and
+    the output meets the layer bar."""
+    from robustgemq_amd import ops
+    _say(f"[layer] one-token forward routing: {name}")
+    cfg, w, block, dense = _layer(name)
+    x = make_x(cfg, 1, seed=11)
+    ref, ref_lg, ref_idx, ref_w = _oracle(cfg, w, dense, x)
+    layer = block._layer
+    xd = x.to("cuda")
+    out32, lg = layer.forward(xd, out_dtype=torch.float32, want_logits=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(lg.float().cpu().numpy().view(np.uint32), ref_lg.view(np.uint32))
+    k, E, ns = layer.top_k, layer.n_experts, layer.n_shared
+    offs, ws = layer.workspace_layout(1), layer._ws
+
+    def arr(i, n, dt=torch.int32):
+        return ws[offs[i]:offs[i] + 4 * n].view(dt).cpu().numpy()
+
+    np.testing.assert_array_equal(arr(0, k), ref_idx.reshape(-1))
+    _, _, w2 = ops.route(xd, layer.gate_w, k, layer.norm_topk, logit_bias=layer.logit_bias)
+    wt = arr(1, k, torch.float32)
+    np.testing.assert_array_equal(wt.view(np.uint32), to_np(w2).reshape(-1).view(np.uint32))
+    np.testing.assert_allclose(wt, ref_w.reshape(-1), rtol=2e-6, atol=1e-7)
+    ref_perm = orr.permute(ref_idx, E, ns)
+    rows = k + ns
+    for i, key, n in ((2, "counts", E + ns), (3, "offsets", E + ns + 1), (4, "row_token", rows),
+                      (5, "row_pair", k), (6, "inv_perm", k)):
+        np.testing.assert_array_equal(arr(i, n), ref_perm[key], err_msg=key)
+    nt = int(arr(8, 1)[0])
+    assert nt == rows
+    tiles = arr(7, 4 * nt).reshape(nt, 4)
+    want = np.stack([np.concatenate([np.sort(ref_idx.reshape(-1)), E + np.arange(ns)]), np.arange(rows),
+                     np.ones(rows), np.zeros(rows)], 1).astype(np.int32)
+    np.testing.assert_array_equal(tiles, want)
+    got = to_np(out32)
+    assert relative_error(got, ref) <= REL_L2 and float(np.abs(got - ref).max()) <= MAX_ABS
+
+
 def make_x(cfg, T, seed=5):
     from robustgemq_amd.synthetic import make_inputs
     return make_inputs(cfg, T, seed=seed)
