@@ -5,10 +5,12 @@ Workload (configs[1] of BASELINE.json): OLMoE-1B-7B-shaped layer, hidden 2048,
 (50/25/25) group-64 HQQ weights, fp16 activations, synthetic data.  A step is
 one full layer forward (route, permute, grouped gate/up + SiLU*mul, grouped
 down, combine) over a 2048-token prefill batch already resident in HBM;
-`value` is prefill tokens/s.  The same run also reports prefill at 512 tokens,
-decode at batch 1 / 8 / 32 of this layer and at batch 1 / 16 / 64 of the
-Mixtral-shaped layer of configs[4] (HBM-bound; graph-replayed, as the
-reference times decode under CUDA graphs), the live roofline of the dominant
+`value` is prefill tokens/s, measured after a short untimed clock settle.
+The same run also reports prefill at 512 tokens, decode at batch 1 / 8 / 32 of
+this layer and at batch 1 / 16 / 64 of the Mixtral-shaped layer of configs[4]
+(HBM-bound; a stack of distinct layers whose experts exceed the last-level
+cache, graph-replayed, as the reference times decode under CUDA graphs; per
+layer), the live roofline of the dominant
 kernel (the grouped gate/up GEMM, MFMA-bound at this size) with its HBM
 traffic from the committed rocprofv3 counter summary, and the CPU baseline:
 the oracle's fp32 dequantize-then-matmul expert loop on a bounded token
@@ -30,6 +32,8 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer prefill+decode tokens/sec on 1 GPU; % HBM BW / % MFMA peak"
 PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 PEAK_HBM_GBS = 8000.0
+SETTLE_S = 0.3  # untimed layer forwards before the first measurement
+DECODE_LAYERS = 4  # distinct layers in the decode stack of the headline config
 
 
 def parse():
@@ -115,7 +119,7 @@ def main():
     x = make_inputs(cfg, T, seed=0).to(dev)
     stream = torch.cuda.current_stream(dev)
 
-    # ---------------- the timed step: full layer forward, T tokens
+    # ---------------- the step: full layer forward, T tokens
     out = torch.empty((T, cfg.hidden), dtype=cfg.act_dtype, device=dev)
     logits = torch.empty((T, cfg.n_experts), dtype=torch.float32 if cfg.family == "deepseekv2" else cfg.act_dtype,
                          device=dev)
@@ -123,6 +127,19 @@ def main():
     def step():
         layer.forward(x, out=out, logits=logits)
 
+    # Clock settle: the GPU raises its clocks over the first tens of ms of
+    # load (a cold 20-step loop reads ~15% slower than the same loop warm), so
+    # the layer runs untimed for SETTLE_S before any measurement; every number
+    # below is a sustained rate.
+    settle_steps = 0
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        settle_steps += 10
+
+    # ---------------- the timed steps (headline): W warmup, then exactly K
     log(f"[bench] prefill T={T}: warmup {args.warmup}, steps {args.steps}")
     for _ in range(args.warmup):
         step()
@@ -183,6 +200,7 @@ def main():
                 "traffic_source": tsrc}
     layer_flops = flops(cfg, T)
     extra = {
+        "settle": {"seconds": SETTLE_S, "steps": settle_steps},
         "stage_ms": {k: round(v, 4) for k, v in kt.items()},
         "layer_tflops": round(layer_flops / (ms_per_step * 1e-3) / 1e12, 2),
         "down_tflops": round(dn_flops / (kt["down"] * 1e-3) / 1e12, 2),
@@ -196,7 +214,16 @@ def main():
         ms = time_events(lambda: layer.forward(xp, want_logits=False), args.steps, args.warmup, stream)
         runs[f"prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4)}
     if not args.no_decode:
-        runs.update(decode_runs(cfg, layer, cfg.runs.get("decode", ()), args, stream, ""))
+        # four distinct layers (seeds 0..3, ~600 MB of experts: more than the
+        # 256 MB last-level cache) so a decode step streams its experts from HBM
+        extra_layers = []
+        for sd in range(1, DECODE_LAYERS):
+            ew = make_weights(cfg, seed=sd, quant_device=dev)
+            extra_layers.append(build_block(cfg, ew, device=dev)._layer)
+            del ew
+        runs.update(decode_runs(cfg, [layer] + extra_layers, cfg.runs.get("decode", ()), args, stream, ""))
+        del extra_layers
+        torch.cuda.empty_cache()
     if not args.no_mixtral and args.config != "mixtral_mixed":
         # the HBM-bound decode (two 55-100 MB experts per token) and
         # the 16-layer stack at 1024-token prefill
@@ -205,7 +232,11 @@ def main():
         mw = make_weights(mcfg, seed=0, quant_device=dev)
         mlayer = build_block(mcfg, mw, device=dev)._layer
         del mw
-        runs.update(decode_runs(mcfg, mlayer, mcfg.runs.get("decode", ()), args, stream, "mixtral_"))
+        mw2 = make_weights(mcfg, seed=1, quant_device=dev)
+        mlayer2 = build_block(mcfg, mw2, device=dev)._layer  # two layers: 1.2 GB of experts
+        del mw2
+        runs.update(decode_runs(mcfg, [mlayer, mlayer2], mcfg.runs.get("decode", ()), args, stream, "mixtral_"))
+        del mlayer2
         runs.update(stack_run(mcfg, mlayer, 16, 1024, args, stream))
         del mlayer
         torch.cuda.empty_cache()
@@ -274,43 +305,63 @@ def stack_run(cfg, layer, n_layers, T, args, stream):
         "weights": "one synthetic layer's weights reused by all layers"}}
 
 
-def decode_runs(cfg, layer, batches, args, stream, tag):
-    """Decode steps (one layer forward of B tokens) replayed from a CUDA graph,
-    as the reference times decode under CUDA graphs; each replay's output is
-    checked against the eager one.  HBM fraction = algorithmic bytes (packed
-    codes + scale/zero of the hit experts, router, activations) / time / 8 TB/s."""
+def decode_runs(cfg, layers, batches, args, stream, tag):
+    """Decode steps of a stack of distinct layers (each layer's output feeds
+    the next, as in a model), captured in one CUDA graph and replayed, as the
+    reference times decode under CUDA graphs; per-layer time = replay time / L.
+    The layers' experts together exceed the 256 MB last-level cache, so the
+    weights come from HBM rather than from the previous replay's cache lines.
+    Each replay's output is checked against the eager stack.  HBM fraction =
+    algorithmic bytes per layer (packed codes + scale/zero of the hit experts,
+    router, activations; averaged over the stack) / per-layer time / 8 TB/s."""
     import torch
 
     from robustgemq_amd import ops
     from robustgemq_amd.synthetic import make_inputs
     dev = torch.device("cuda:0")
     out = {}
+    L = len(layers)
     for B in batches:
         xb = make_inputs(cfg, B, seed=2).to(dev)
-        ob = torch.empty((B, cfg.hidden), dtype=cfg.act_dtype, device=dev)
-        layer.forward(xb, out=ob, want_logits=False)  # sizes the workspace before capture
+        hs = [torch.empty((B, cfg.hidden), dtype=cfg.act_dtype, device=dev) for _ in range(L)]
+
+        def stack():
+            h = xb
+            for i, ly in enumerate(layers):
+                ly.forward(h, out=hs[i], want_logits=False)
+                h = hs[i]
+
+        stack()  # sizes the workspaces before capture
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(dev)
         s.wait_stream(stream)
         with torch.cuda.stream(s):
-            layer.forward(xb, out=ob, want_logits=False)
+            stack()
             torch.cuda.synchronize()
             with torch.cuda.graph(g, stream=s):
-                layer.forward(xb, out=ob, want_logits=False)
+                stack()
         stream.wait_stream(s)
-        ref = ob.clone()
-        ms_graph = time_events(g.replay, args.steps * 5, args.warmup, stream)
-        assert torch.equal(ob, ref), "graph replay changed the decode output"
-        ms_eager = time_events(lambda: layer.forward(xb, out=ob, want_logits=False), args.steps, args.warmup,
-                               stream)
-        idx_b = ops.route(xb, layer.gate_w, layer.top_k, layer.norm_topk, logits=False,
-                          logit_bias=layer.logit_bias)[1]
-        hit_b = sorted(set(idx_b.cpu().numpy().reshape(-1).tolist()))
-        bytes_b = (layer.w1.weight_bytes(hit_b) + layer.w3.weight_bytes(hit_b) + layer.w2.weight_bytes(hit_b)
-                   + cfg.n_experts * cfg.hidden * 2 + 2 * B * cfg.hidden * 2)
+        ref = hs[-1].clone()
+        t_end = time.perf_counter() + 0.2  # clock settle (untimed replays)
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                g.replay()
+            torch.cuda.synchronize()
+        ms_graph = time_events(g.replay, args.steps * 5, args.warmup, stream) / L
+        assert torch.equal(hs[-1], ref), "graph replay changed the decode output"
+        ms_eager = time_events(stack, args.steps, args.warmup, stream) / L
+        bytes_b = 0
+        h = xb
+        for i, ly in enumerate(layers):
+            idx_b = ops.route(h, ly.gate_w, ly.top_k, ly.norm_topk, logits=False, logit_bias=ly.logit_bias)[1]
+            hit_b = sorted(set(idx_b.cpu().numpy().reshape(-1).tolist()))
+            bytes_b += (ly.w1.weight_bytes(hit_b) + ly.w3.weight_bytes(hit_b) + ly.w2.weight_bytes(hit_b)
+                        + cfg.n_experts * cfg.hidden * 2 + 2 * B * cfg.hidden * 2)
+            h = hs[i]
+        bytes_b //= L
         out[f"{tag}decode_B{B}"] = {"tokens_per_s": round(B / (ms_graph * 1e-3), 1), "ms_graph": round(ms_graph, 4),
-                                     "ms_eager": round(ms_eager, 4), "hit_experts": len(hit_b),
+                                     "ms_eager": round(ms_eager, 4), "layers": L,
                                      "alg_bytes": bytes_b,
                                      "hbm_frac_layer": round(bytes_b / (ms_graph * 1e-3) / (PEAK_HBM_GBS * 1e9), 4)}
     return out
