@@ -234,6 +234,14 @@ int moeq_gemm_tile_n(int bm, int epilogue);
  * max_tiles, dtype of the grouped down-projection output}. */
 int moeq_moe_plan(const moeq_moe *m, int64_t T, int32_t *out4);
 
+/* moeq_moe_forward that also records two HIP events (hipEvent_t, passed as
+ * void *) on `stream`, just before and just after its gate/up grouped-GEMM
+ * launch, so a benchmark can time that kernel inside the layer.  Benchmark
+ * introspection; no reference counterpart. */
+int moeq_moe_forward_timed(const moeq_moe *m, const void *x, int64_t T, void *out,
+                           int out_dtype, void *logits_out, void *ws, size_t ws_bytes,
+                           void *stream, void *ev_gate_up_begin, void *ev_gate_up_end);
+
 /* Byte offsets, in the workspace of moeq_moe_forward for T tokens, of the
  * routing and permutation it leaves there: out9 = {idx, w, counts, offsets,
  * row_token, row_pair, inv_perm, tiles, n_tiles} (layouts as moeq_route and

@@ -26,6 +26,11 @@ int check_launch(const char *what) {
   return MOEQ_OK;
 }
 
+static int hip_ok(hipError_t e, const char *what) {
+  if (e != hipSuccess) return fail(MOEQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MOEQ_OK;
+}
+
 // Launch plan of one layer forward; a pure function of (layer, T) so the
 // workspace query and the forward agree.
 struct Plan {
@@ -123,9 +128,11 @@ extern "C" size_t moeq_moe_workspace_size(const moeq_moe *m, int64_t T) {
   return make_plan(m, T).total;
 }
 
-extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out,
-                                int out_dtype, void *logits_out, void *ws, size_t ws_bytes,
-                                void *stream) {
+// The layer forward; ev0 / ev1 (may be null) are recorded on the stream
+// just before and just after the gate/up launch.
+static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, int out_dtype,
+                       void *logits_out, void *ws, size_t ws_bytes, void *stream, hipEvent_t ev0,
+                       hipEvent_t ev1) {
   int rc = check_layer(m);
   if (rc) return rc;
   if (!x || !out) return fail(MOEQ_ERR_INVALID, "moe: null x/out");
@@ -226,8 +233,10 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
   gu.ldo = m->inter;
   gu.splits = 1;
   gu.split_stride = 0;
+  if (ev0 && (rc = hip_ok(hipEventRecord(ev0, as_stream(stream)), "moe: event record"))) return rc;
   rc = moeq_grouped_gemm(&gu, &m->w1, &m->w3, stream);
   if (rc) return rc;
+  if (ev1 && (rc = hip_ok(hipEventRecord(ev1, as_stream(stream)), "moe: event record"))) return rc;
 
   moeq_gemm dn = gu;
   dn.a = at(p.off_h);
@@ -245,6 +254,22 @@ extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, voi
 
   return moeq_combine(at(p.off_y), p.y_dtype, p.splits, p.rows * m->hidden, m->hidden, inv, w, T,
                       m->top_k, m->n_shared, m->hidden, out, out_dtype, stream);
+}
+
+extern "C" int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out,
+                                int out_dtype, void *logits_out, void *ws, size_t ws_bytes,
+                                void *stream) {
+  return moe_forward(m, x, T, out, out_dtype, logits_out, ws, ws_bytes, stream, nullptr, nullptr);
+}
+
+// Benchmark introspection (not a reference interface): moeq_moe_forward that
+// also records two HIP events around its gate/up launch.
+extern "C" int moeq_moe_forward_timed(const moeq_moe *m, const void *x, int64_t T, void *out,
+                                      int out_dtype, void *logits_out, void *ws, size_t ws_bytes,
+                                      void *stream, void *ev_gate_up_begin, void *ev_gate_up_end) {
+  if (!ev_gate_up_begin || !ev_gate_up_end) return fail(MOEQ_ERR_INVALID, "moe_forward_timed: null event");
+  return moe_forward(m, x, T, out, out_dtype, logits_out, ws, ws_bytes, stream,
+                     static_cast<hipEvent_t>(ev_gate_up_begin), static_cast<hipEvent_t>(ev_gate_up_end));
 }
 
 // Workspace introspection for tests (not a reference interface): byte

@@ -170,8 +170,10 @@ class MoELayer:
             self._ws = torch.empty(need, dtype=torch.uint8, device=device)
         return self._ws
 
-    def forward(self, x, out_dtype=None, want_logits=True, out=None, logits=None):
-        """x [T, H] -> (out [T, H], logits [T, E] or None)."""
+    def forward(self, x, out_dtype=None, want_logits=True, out=None, logits=None, gate_up_events=None):
+        """x [T, H] -> (out [T, H], logits [T, E] or None).  gate_up_events:
+        optional pair of recorded torch.cuda.Event, re-recorded on the
+        current stream just before and after the gate/up launch."""
         assert x.dim() == 2 and x.shape[1] == self.hidden, x.shape
         if x.dtype != self.act_dtype:
             raise TypeError(f"activations are {x.dtype}, layer expects {self.act_dtype}")
@@ -185,6 +187,15 @@ class MoELayer:
             ldt = torch.float32 if self.gate_w.dtype == torch.float32 else self.act_dtype
             logits = torch.empty((T, self.n_experts), dtype=ldt, device=dev)
         ws = self.workspace(T, dev)
+        if gate_up_events is not None:
+            e0, e1 = (e._as_parameter_ for e in gate_up_events)
+            if not e0.value or not e1.value:
+                raise ValueError("gate_up_events must have been recorded once (torch creates them lazily)")
+            L.check(L.lib().moeq_moe_forward_timed(self.desc, L.ptr(x), T, L.ptr(out), L.dtype_code(odt),
+                                                   L.ptr(logits) if want_logits else None, L.ptr(ws),
+                                                   ws.numel(), L.stream_handle(dev), e0, e1),
+                    "moeq_moe_forward_timed")
+            return out, (logits if want_logits else None)
         L.check(L.lib().moeq_moe_forward(self.desc, L.ptr(x), T, L.ptr(out), L.dtype_code(odt),
                                          L.ptr(logits) if want_logits else None, L.ptr(ws), ws.numel(),
                                          L.stream_handle(dev)), "moeq_moe_forward")

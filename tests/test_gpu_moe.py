@@ -174,6 +174,23 @@ def test_one_token_forward_routing(device, name):
     assert relative_error(got, ref) <= REL_L2 and float(np.abs(got - ref).max()) <= MAX_ABS
 
 
+def test_forward_timed_matches_forward(device):
+    """moeq_moe_forward_timed (benchmark introspection) gives the forward's
+    output bit for bit and brackets the gate/up launch with its two events."""
+    _say("[layer] forward_timed == forward")
+    cfg, w, block, dense = _layer("olmoe_mixed")
+    layer = block._layer
+    x = make_x(cfg, 256, seed=3).to("cuda")
+    ref, _ = layer.forward(x, want_logits=False)
+    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    for e in ev:
+        e.record()
+    got, _ = layer.forward(x, want_logits=False, gate_up_events=ev)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, got)
+    assert ev[0].elapsed_time(ev[1]) > 0
+
+
 def make_x(cfg, T, seed=5):
     from robustgemq_amd.synthetic import make_inputs
     return make_inputs(cfg, T, seed=seed)
