@@ -106,3 +106,26 @@ def test_replace_linear_recursive(device):
     x = torch.randn(3, K, device=device).half()
     ref = x.float().cpu().numpy() @ dense.T
     assert relative_error(to_np(model(x)).astype(np.float32), ref) <= REL_L2
+
+
+@pytest.mark.parametrize("nbits", [1, 2, 3, 4])
+def test_hqq_checkpoint_linears(device, tmp_path, nbits):
+    """HQQ layer states (packed as hqq's BitPack, scale/zero in the meta) saved
+    to a file and loaded without hqq: the linears equal the dequantized
+    weight's matmul at the expert path's bar, and the name filter applies."""
+    from robustgemq_amd import hqq_format as hf
+    print(f"[linear] HQQ checkpoint load, nbits={nbits}", flush=True)
+    N, K, g = 256, 512, 64
+    t, dense = _weights(N, K, nbits, g, seed=31 + nbits)
+    bias = torch.from_numpy((np.random.default_rng(nbits).standard_normal(N) * 0.1).astype(np.float16))
+    st = hf.HQQLinearState.from_quantized(t.Q, t.scales, t.zeros, t.shape, nbits, g, bias=bias)
+    p = tmp_path / "qmodel.pt"
+    torch.save({"layers.0.mlp.down_proj": {"W_q": st.W_q, "meta": st.meta, "bias": bias},
+                "layers.0.input_layernorm": {"weight": torch.ones(K)}}, p)
+    lins = hf.load_hqq_linears(p, device=device)
+    assert list(lins) == ["layers.0.mlp.down_proj"]
+    assert hf.load_hqq_linears(p, device=device, names=lambda n: "attn" in n) == {}
+    x = torch.from_numpy((np.random.default_rng(7).standard_normal((5, K)) * 0.5).astype(np.float16))
+    got = to_np(lins["layers.0.mlp.down_proj"](x.to(device))).astype(np.float32)
+    ref = x.float().numpy() @ dense.T + bias.float().numpy()
+    assert relative_error(got, ref) <= REL_L2 and float(np.abs(got - ref).max()) <= MAX_ABS
