@@ -47,7 +47,11 @@ _FORMAT = {
 def pack(Q, nbits):
     """Codes Q [R, g] (integers in 0 .. 2**nbits - 1) -> packed W_q."""
     S, b, dt = _FORMAT[BIT_TO_PACKING[int(nbits)]]
+    if Q.is_floating_point() and not torch.equal(Q, Q.round()):
+        raise ValueError("codes must be integers")
     Q = Q.to(torch.int32)
+    if Q.numel() and (int(Q.min()) < 0 or int(Q.max()) >= (1 << b)):
+        raise ValueError(f"codes outside 0..{(1 << b) - 1} for {nbits}-bit packing")
     R = Q.shape[0]
     if dt == torch.int32:
         rows = S * math.ceil(R / S)

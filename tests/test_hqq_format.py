@@ -71,6 +71,15 @@ def test_codes_cut_and_layer_state(nbits):
         hf.HQQLinearState.from_state_dict({"W_q": st.W_q, "nbits": nbits})
 
 
+def test_out_of_range_codes_are_refused():
+    with pytest.raises(ValueError):
+        hf.pack(torch.tensor([[4], [0], [1], [2]]), 2)  # 4 does not fit 2 bits
+    with pytest.raises(ValueError):
+        hf.pack(torch.tensor([[-1], [0]]), 4)
+    with pytest.raises(ValueError):
+        hf.pack(torch.tensor([[0.5], [1.0]]), 4)
+
+
 def test_axis_other_than_one_is_refused():
     st = hf.HQQLinearState.from_quantized(torch.zeros(8, 4), torch.ones(8, 1), torch.zeros(8, 1), (8, 4), 4, 4)
     st.meta["axis"] = 0
