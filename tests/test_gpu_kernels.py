@@ -54,6 +54,7 @@ def test_pack_and_repack_bit_exact(device, nbits):
 # ------------------------------------------------------------------ routing
 @pytest.mark.parametrize("gate", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("T,H,E,k,norm", [(1, 2048, 64, 8, False), (333, 2048, 64, 8, False),
+                                         (2048, 2048, 64, 8, False),
                                          (257, 2048, 128, 8, True), (64, 4096, 8, 2, True),
                                          (40, 1536, 64, 6, False), (16, 512, 8, 2, False),
                                          (300, 1000, 60, 4, True), (130, 768, 256, 8, False)])

@@ -191,6 +191,29 @@ def test_forward_timed_matches_forward(device):
     assert ev[0].elapsed_time(ev[1]) > 0
 
 
+def test_full_size_prefill_rows_match_oracle(device):
+    """BASELINE configs[1] at its benchmark size, T = 2048: the logits and
+    output rows of 64 sampled tokens against the oracle run on those tokens
+    alone (a token's logits and output depend on that token only), and a
+    second forward is bit-identical."""
+    _say("[layer] olmoe_mixed T=2048 sampled rows vs oracle, determinism")
+    cfg, w, block, dense = _layer("olmoe_mixed")
+    layer = block._layer
+    T = 2048
+    x = make_x(cfg, T, seed=21)
+    xd = x.to("cuda")
+    out32, lg = layer.forward(xd, out_dtype=torch.float32, want_logits=True)
+    sel = np.sort(np.random.default_rng(0).choice(T, 64, replace=False))
+    ref, ref_lg, _, _ = _oracle(cfg, w, dense, x[torch.from_numpy(sel)])
+    np.testing.assert_array_equal(lg.float().cpu().numpy()[sel].view(np.uint32), ref_lg.view(np.uint32))
+    got = to_np(out32)[sel]
+    err, mx = relative_error(got, ref), float(np.abs(got - ref).max())
+    _say(f"    rel-L2 {err:.3e} max-abs {mx:.3e}")
+    assert err <= REL_L2 and mx <= MAX_ABS
+    again, _ = layer.forward(xd, out_dtype=torch.float32, want_logits=False)
+    assert torch.equal(out32, again)
+
+
 def make_x(cfg, T, seed=5):
     from robustgemq_amd.synthetic import make_inputs
     return make_inputs(cfg, T, seed=seed)
