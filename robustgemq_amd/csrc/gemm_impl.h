@@ -448,13 +448,24 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
   // The grid is sized for the host-side bound on row tiles; blocks past the
   // real count (read from the device schedule) exit together.  Work-groups
   // are dealt to the 8 XCDs round-robin, so the live ones are renumbered to
-  // give each XCD a contiguous run of tiles (same row tile with neighbouring
+  // give each XCD runs of neighbouring tiles (same row tile with neighbouring
   // column tiles, then the next row tile of the same expert) sharing its L2.
   const unsigned V = unsigned(*g.n_tiles) * unsigned(g.n_ntiles);
   const unsigned b = blockIdx.x;
   if (b >= V) return;
+  // XCD x = b % 8 takes its k-th block as block L of the tile list: the list
+  // (first V8 = V & ~7 blocks) is cut into 8 * XG segments of ln blocks and
+  // XCD x gets segments x, x + 8, x + 16, ... (XG of them), so tiles of
+  // different sizes (Zipf routing, remainder tiles) spread over the XCDs
+  // while each segment keeps neighbouring tiles together; the per % XG blocks
+  // left over go to the XCDs as equal runs after the segments.
   const unsigned V8 = V & ~7u;
-  const unsigned L = b < V8 ? (b & 7u) * (V8 >> 3) + (b >> 3) : b;
+  unsigned L = b;
+  if (b < V8) {
+    constexpr unsigned XG = 8;
+    const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3, ln = per / XG;
+    L = k < XG * ln ? ((k / ln) * 8u + x) * ln + k % ln : 8u * XG * ln + x * (per - XG * ln) + (k - XG * ln);
+  }
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
   // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * NB * 4
