@@ -57,6 +57,20 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def settle(fn, seconds):
+    """Runs fn untimed for `seconds` (the GPU raises its clocks over the first
+    tens of ms of load); returns the number of calls."""
+    import torch
+    n = 0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        n += 10
+    return n
+
+
 def time_events(fn, steps, warmup, stream):
     import torch
     for _ in range(warmup):
@@ -131,13 +145,7 @@ def main():
     # load (a cold 20-step loop reads ~15% slower than the same loop warm), so
     # the layer runs untimed for SETTLE_S before any measurement; every number
     # below is a sustained rate.
-    settle_steps = 0
-    t_end = time.perf_counter() + SETTLE_S
-    while time.perf_counter() < t_end:
-        for _ in range(10):
-            step()
-        torch.cuda.synchronize()
-        settle_steps += 10
+    settle_steps = settle(step, SETTLE_S)
 
     # ---------------- the timed steps (headline): W warmup, then exactly K.
     # Each timed step also records a pair of HIP events around its gate/up
@@ -220,6 +228,7 @@ def main():
     runs = {}
     for tp in [t for t in cfg.runs.get("prefill", ()) if t != T]:
         xp = make_inputs(cfg, tp, seed=1).to(dev)
+        settle(lambda: layer.forward(xp, want_logits=False), 0.2)
         ms = time_events(lambda: layer.forward(xp, want_logits=False), args.steps, args.warmup, stream)
         runs[f"prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4)}
     if not args.no_decode:
@@ -261,6 +270,7 @@ def main():
             del ow
             for tp in ocfg.runs.get("prefill", ()):
                 xp = make_inputs(ocfg, tp, seed=1).to(dev)
+                settle(lambda: olayer.forward(xp, want_logits=False), 0.2)
                 ms = time_events(lambda: olayer.forward(xp, want_logits=False), args.steps, args.warmup, stream)
                 tf = flops(ocfg, tp) / (ms * 1e-3) / 1e12
                 runs[f"{name}_prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4),
@@ -306,6 +316,7 @@ def stack_run(cfg, layer, n_layers, T, args, stream):
             layer.forward(h, out=bufs[i & 1], want_logits=False)
             h = bufs[i & 1]
 
+    settle(stack, 0.2)
     ms = time_events(stack, max(2, args.steps // 4), 1, stream)
     tf = n_layers * flops(cfg, T) / (ms * 1e-3) / 1e12
     return {f"mixtral_stack{n_layers}_prefill_T{T}": {
@@ -352,11 +363,7 @@ def decode_runs(cfg, layers, batches, args, stream, tag):
                 stack()
         stream.wait_stream(s)
         ref = hs[-1].clone()
-        t_end = time.perf_counter() + 0.2  # clock settle (untimed replays)
-        while time.perf_counter() < t_end:
-            for _ in range(20):
-                g.replay()
-            torch.cuda.synchronize()
+        settle(g.replay, 0.2)
         ms_graph = time_events(g.replay, args.steps * 5, args.warmup, stream) / L
         assert torch.equal(hs[-1], ref), "graph replay changed the decode output"
         ms_eager = time_events(stack, args.steps, args.warmup, stream) / L
