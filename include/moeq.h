@@ -138,9 +138,11 @@ int moeq_route_from_logits(const void *logits, int dtype, int64_t T, int E,
  *   inv_perm[T*top_k]                row of each (t, slot) pair,
  *   tiles[max_tiles*4]               (expert, row_start, row_count, 0): each
  *                                    expert's m rows split into
- *                                    ceil(m / moeq_tile_rows(bm)) tiles of
- *                                    near-equal size (counts differ by at
- *                                    most one), in expert order,
+ *                                    ceil(m / moeq_tile_rows(bm)) tiles at
+ *                                    16-row boundaries, the first ones of
+ *                                    the class's largest block count, the
+ *                                    rest of the next lower count (see
+ *                                    moeq_tile_rows), in expert order,
  *   n_tiles[1].
  * max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm).
  * Replaces the one_hot / nonzero / torch.where grouping and its host syncs,

@@ -26,11 +26,20 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Row capacity of one grouped-GEMM tile of class bm: the schedule splits an
-// expert's m rows into ceil(m / cap) near-equal tiles, so the prefill classes
-// leave room above their nominal height (an expert a little past 2 x 128 rows
-// still takes two tiles, not three).  0 for an unknown class.
+// expert's m rows into ceil(m / cap) tiles, so the prefill classes leave room
+// above their nominal height (an expert a little past 2 x 128 rows still
+// takes two tiles, not three).  0 for an unknown class.
 __host__ __device__ constexpr int tile_rows(int bm) {
   return bm == 16 ? 16 : bm == 32 ? 48 : bm == 64 ? 96 : bm == 128 ? 160 : bm == 256 ? 256 : 0;
+}
+
+// The grouped GEMM instantiates, per class, kernel variants for 16-row block
+// counts {1} (bm 16), {2, 3} (32), {2, 4, 6} (64), {2, 4, 8, 10} (128) and
+// {2, 4, 8, 16} (256); a tile of b blocks runs the smallest count >= b.  The
+// schedule cuts experts into tiles of the largest count and of the one below
+// it, returned here.
+__host__ __device__ constexpr int tile_blocks_below(int bm) {
+  return bm == 16 ? 1 : bm == 32 ? 2 : bm == 64 ? 4 : bm == 128 ? 8 : bm == 256 ? 8 : 0;
 }
 
 // ------------------------------------------------------- device helpers

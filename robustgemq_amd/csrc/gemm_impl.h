@@ -4,7 +4,7 @@
 //
 // One launch covers every (row tile, column tile) of every expert; the row
 // tiles come from the device-side schedule written by moeq_permute (each
-// expert's rows in near-equal tiles of at most tile_rows(BM) rows), so no
+// expert's rows in tiles of at most tile_rows(BM) rows), so no
 // host synchronisation is needed.  A block has NW waves; wave w owns NB * 16 output columns and all
 // active rows of the tile.  Per 128-deep K chunk:
 //   A (activations, gathered rows): BM >= 32 -> copied global -> LDS with

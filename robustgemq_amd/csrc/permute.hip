@@ -95,10 +95,18 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
                         int32_t *n_tiles, int *sh, int *s_off) {
   const int e = threadIdx.x, Et = E + n_shared;
   const int m = e < Et ? c : 0;
-  // an expert's rows in ceil(m / cap) tiles of near-equal size; experts in
-  // order, so the tiles sharing an expert's weights are dispatched together
+  // An expert's rows in ceil(m / cap) tiles cut at 16-row block boundaries;
+  // experts in order, so the tiles sharing an expert's weights are dispatched
+  // together.  A tile of b blocks runs the kernel variant with the smallest
+  // block count >= b, so the first x tiles take the class's largest count
+  // smax and the rest the next lower count s2, x being the fewest that hold
+  // all B blocks: an expert of 17 blocks at smax = 10 runs 10 + 8 = 18
+  // blocks, where two halves of 8.5 blocks would run 10 + 10.
   const int cap = tile_rows(bm);
-  const int nt = (m + cap - 1) / cap;
+  const int smax = cap / 16, s2 = tile_blocks_below(bm);
+  const int B = (m + 15) / 16;
+  const int nt = (B + smax - 1) / smax;
+  const int x = smax == s2 ? nt : min(nt, max(0, (B - s2 * nt + (smax - s2) - 1) / (smax - s2)));
   int tot_rows, tot_tiles;
   const int off = block_exclusive_scan(m, sh, &tot_rows);
   const int tb = block_exclusive_scan(nt, sh, &tot_tiles);
@@ -114,7 +122,11 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
     *n_tiles = min(tot_tiles, max_tiles);
   }
   for (int j = 0; j < nt && tb + j < max_tiles; ++j) {
-    const int r0 = int(int64_t(m) * j / nt), r1 = int(int64_t(m) * (j + 1) / nt);
+    // (nt - 1) * smax < B, so every tile before the last is full and the
+    // last one holds at least one block
+    const int b0 = j < x ? j * smax : x * smax + (j - x) * s2;
+    const int b1 = min(b0 + (j < x ? smax : s2), B);
+    const int r0 = 16 * b0, r1 = min(16 * b1, m);
     int32_t *tp = tiles + 4 * (tb + j);
     tp[0] = e;
     tp[1] = off + r0;

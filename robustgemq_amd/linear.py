@@ -29,6 +29,28 @@ def _bm_for_rows(m):
     return 16 if m <= 16 else 32 if m <= 32 else 64 if m <= 64 else 128
 
 
+# Largest 16-row block count of a tile class and the next lower count the
+# grouped GEMM has a variant for (tile_rows / tile_blocks_below in csrc/common.h).
+_BLOCKS = {16: (1, 1), 32: (3, 2), 64: (6, 4), 128: (10, 8), 256: (16, 8)}
+
+
+def split_rows(m, bm):
+    """(row_start, row_count) of the tiles one expert's m rows take in class
+    bm, cut as the device schedule of moeq_permute cuts them: ceil(m / cap)
+    tiles at 16-row boundaries, the first x holding the largest block count
+    and the rest the next lower one, x the fewest that hold every block."""
+    smax, s2 = _BLOCKS[bm]
+    B = -(-m // 16)
+    nt = -(-B // smax)
+    x = nt if smax == s2 else min(nt, max(0, -(-(B - s2 * nt) // (smax - s2))))
+    out, b0 = [], 0
+    for j in range(nt):
+        b1 = min(b0 + (smax if j < x else s2), B)
+        out.append((16 * b0, min(16 * b1, m) - 16 * b0))
+        b0 = b1
+    return out
+
+
 class QuantLinear(nn.Module):
     """y = x @ dequant(W)^T (+ bias) for x [..., in_features]."""
 
@@ -85,15 +107,13 @@ class QuantLinear(nn.Module):
 
     # -- forward ------------------------------------------------------------
     def _tile_list(self, M, dev):
-        """Rows 0..M-1 of the single expert in near-equal tiles of at most
-        moeq_tile_rows(bm) rows (the schedule moeq_permute writes)."""
+        """Rows 0..M-1 of the single expert in tiles of at most
+        moeq_tile_rows(bm) rows, cut as moeq_permute cuts an expert."""
         key = (M, dev)
         if key not in self._tiles:
             bm = _bm_for_rows(M)
-            cap = L.lib().moeq_tile_rows(bm)
-            nt = -(-M // cap)
-            bounds = [M * j // nt for j in range(nt + 1)]
-            tiles = [(0, bounds[j], bounds[j + 1] - bounds[j], 0) for j in range(nt)]
+            tiles = [(0, r0, rc, 0) for r0, rc in split_rows(M, bm)]
+            nt = len(tiles)
             self._tiles[key] = (bm, torch.tensor(tiles, dtype=torch.int32, device=dev),
                                 torch.tensor([nt], dtype=torch.int32, device=dev), nt)
         return self._tiles[key]

@@ -118,14 +118,16 @@ def test_permute_bit_exact(device, T, k, E, S, bm):
         assert ref["offsets"][e] <= r0 and r0 + rc <= ref["offsets"][e + 1]
         covered[r0:r0 + rc] += 1
     assert (covered == 1).all()
-    # each expert's m rows in ceil(m / cap) tiles whose sizes differ by at most one
+    # each expert's m rows in ceil(m / cap) tiles cut at 16-row boundaries,
+    # as the host-side restatement split_rows cuts them
+    from robustgemq_amd.linear import split_rows
     sizes = {}
     for e, r0, rc, _ in tiles:
-        sizes.setdefault(int(e), []).append(int(rc))
+        sizes.setdefault(int(e), []).append((int(r0 - ref["offsets"][e]), int(rc)))
     for e, m in enumerate(ref["counts"]):
         got = sizes.get(e, [])
         assert len(got) == -(-int(m) // cap), (e, m, got)
-        assert not got or max(got) - min(got) <= 1, (e, m, got)
+        assert got == (split_rows(int(m), bm) if m else []), (e, m, got)
 
 
 # ------------------------------------------------------------- grouped GEMM

@@ -146,6 +146,33 @@ def test_tile_rows_classes():
     assert lib.moeq_tile_rows(48) == 0 and lib.moeq_tile_rows(0) == 0
 
 
+def test_tile_split_rule():
+    """Tiles cover an expert's rows once, in ceil(m / cap) tiles of at most cap
+    rows at 16-row boundaries, and never run more 16-row blocks (rounded up to
+    the kernel's variants) than an even split of the rows would."""
+    from robustgemq_amd.linear import split_rows
+    variants = {16: (1,), 32: (2, 3), 64: (2, 4, 6), 128: (2, 4, 8, 10), 256: (2, 4, 8, 16)}
+
+    def run_blocks(rows, bm):
+        b = -(-rows // 16)
+        return min(v for v in variants[bm] if v >= b)
+
+    lib = L.lib()
+    for bm in (16, 32, 64, 128, 256):
+        cap = lib.moeq_tile_rows(bm)
+        for m in range(1, 3000):
+            t = split_rows(m, bm)
+            assert len(t) == -(-m // cap)
+            assert [r0 for r0, _ in t] == [sum(rc for _, rc in t[:j]) for j in range(len(t))]
+            assert sum(rc for _, rc in t) == m and all(0 < rc <= cap for _, rc in t)
+            assert all(rc % 16 == 0 for _, rc in t[:-1])
+            nt = len(t)
+            even = [m * (j + 1) // nt - m * j // nt for j in range(nt)]
+            assert sum(run_blocks(rc, bm) for _, rc in t) <= sum(run_blocks(rc, bm) for rc in even), (bm, m, t)
+    # an expert of 17 blocks in the 128-row class runs 10 + 8 blocks, not 10 + 10
+    assert split_rows(260, 128) == [(0, 160), (160, 100)]
+
+
 def test_layer_plan_and_workspace():
     lib = L.lib()
     f = 0x1000
