@@ -35,15 +35,16 @@ __global__ __launch_bounds__(256) void topk_from_logits_kernel(
 }
 
 // ---------------------------------------------------------------- prefill
-// Logits and top-k of 8 tokens per work-group.  Wave w takes 8-expert blocks
-// w, w + NWV, ...; each lane runs the 64 chains of an 8 x 8 (token, expert)
-// block over its k set, so every loaded x / w value feeds 8 fused
-// multiply-adds.  The 64 chains are then summed over the lanes by halving
-// exchanges that pair the same lanes in the same order as the xor butterfly
-// (o = 32 .. 1), leaving chain l in lane l with the identical value.  The
-// rounded logits of the 8 tokens meet in LDS, and one wave per token ranks
-// them.
-constexpr int kTT = 8, kEE = 8;
+// Logits and top-k of kTT tokens per work-group (8, or 4 for batches of at
+// most 1024 tokens).  Wave w takes (64 / kTT)-expert blocks w, w + NWV, ...;
+// each lane runs the 64 chains of a kTT x (64 / kTT) (token, expert) block
+// over its k set, so every loaded x value feeds 64 / kTT and every w value
+// kTT fused multiply-adds.  The 64 chains are then summed over the lanes by
+// halving exchanges that pair the same lanes in the same order as the xor
+// butterfly (o = 32 .. 1), leaving chain l in lane l with the identical
+// value, whatever (token, expert) it holds.  The rounded logits of the kTT
+// tokens meet in LDS, and one wave per token ranks them.
+
 
 // One operand row: the 8 values of one k step, as loaded (fp16 / bf16: four
 // packed words; fp32: eight words).
@@ -129,8 +130,11 @@ __device__ __forceinline__ float halving_sum(float (&c)[64]) {
   return a[0];
 }
 
-template <int XDT, int WDT, int NWV, int MAXCH>
+template <int XDT, int WDT, int NWV, int MAXCH, int kTT>
 __global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
+  // kTT tokens x kEE experts per wave pass (64 chains per lane); the chain
+  // order and the lane reduction do not depend on the split
+  constexpr int kEE = 64 / kTT;
   __shared__ float lg[kTT][512];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -246,23 +250,33 @@ __global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
   }
 }
 
-template <int XDT, int WDT, int NWV>
+template <int XDT, int WDT, int NWV, int TT>
 static void launch_logits_topk_nw(const RouteArgs &a, int maxch, hipStream_t s) {
-  dim3 grid(unsigned(cdiv(a.T, kTT))), block(NWV * 64);
+  dim3 grid(unsigned(cdiv(a.T, TT))), block(NWV * 64);
   switch (maxch) {
-    case 1: logits_topk_kernel<XDT, WDT, NWV, 1><<<grid, block, 0, s>>>(a); break;
-    case 2: logits_topk_kernel<XDT, WDT, NWV, 2><<<grid, block, 0, s>>>(a); break;
-    case 4: logits_topk_kernel<XDT, WDT, NWV, 4><<<grid, block, 0, s>>>(a); break;
-    default: logits_topk_kernel<XDT, WDT, NWV, 8><<<grid, block, 0, s>>>(a); break;
+    case 1: logits_topk_kernel<XDT, WDT, NWV, 1, TT><<<grid, block, 0, s>>>(a); break;
+    case 2: logits_topk_kernel<XDT, WDT, NWV, 2, TT><<<grid, block, 0, s>>>(a); break;
+    case 4: logits_topk_kernel<XDT, WDT, NWV, 4, TT><<<grid, block, 0, s>>>(a); break;
+    default: logits_topk_kernel<XDT, WDT, NWV, 8, TT><<<grid, block, 0, s>>>(a); break;
   }
 }
 
+// 8 tokens x 8 experts per wave pass; up to 1024 tokens (at most 128
+// work-groups of 8, half the CUs or fewer) 4 tokens x 16 experts, so twice
+// as many work-groups share the launch.
 template <int XDT, int WDT>
 static void launch_logits_topk_dt(const RouteArgs &a, int maxch, hipStream_t s) {
-  if (a.E <= 8) launch_logits_topk_nw<XDT, WDT, 1>(a, maxch, s);
-  else if (a.E <= 16) launch_logits_topk_nw<XDT, WDT, 2>(a, maxch, s);
-  else if (a.E <= 32) launch_logits_topk_nw<XDT, WDT, 4>(a, maxch, s);
-  else launch_logits_topk_nw<XDT, WDT, 8>(a, maxch, s);
+  if (a.T <= 1024 && a.E > 8) {
+    if (a.E <= 16) launch_logits_topk_nw<XDT, WDT, 1, 4>(a, maxch, s);
+    else if (a.E <= 32) launch_logits_topk_nw<XDT, WDT, 2, 4>(a, maxch, s);
+    else if (a.E <= 64) launch_logits_topk_nw<XDT, WDT, 4, 4>(a, maxch, s);
+    else launch_logits_topk_nw<XDT, WDT, 8, 4>(a, maxch, s);
+    return;
+  }
+  if (a.E <= 8) launch_logits_topk_nw<XDT, WDT, 1, 8>(a, maxch, s);
+  else if (a.E <= 16) launch_logits_topk_nw<XDT, WDT, 2, 8>(a, maxch, s);
+  else if (a.E <= 32) launch_logits_topk_nw<XDT, WDT, 4, 8>(a, maxch, s);
+  else launch_logits_topk_nw<XDT, WDT, 8, 8>(a, maxch, s);
 }
 
 // ---------------------------------------------------------------- one token
