@@ -4,7 +4,7 @@
 // order torch.where walks the [k, T] expert mask in the reference, and stably
 // sorted by expert.  Three paths by batch size (E + n_shared <= 256 for the
 // first two):
-//   * up to 4096 pairs: one work-group holds every expert id in registers,
+//   * up to 1024 pairs: one work-group holds every expert id in registers,
 //     counts, scans and places them (permute_block);
 //   * up to 65536 pairs: one work-group per 512 positions counts its chunk
 //     (chunk_hist), then every work-group sums the chunk counts itself and
@@ -242,6 +242,12 @@ constexpr int kFusedWaves = 16;
 constexpr int kFusedMaxPPL = 4;
 constexpr int kFusedPairs = kFusedWaves * 64 * kFusedMaxPPL;
 constexpr int kFusedExperts = 256;
+// moeq_permute keeps batches of at most this many pairs in one work-group
+// and gives larger ones to the two chunked launches below: at 4096 pairs the
+// single work-group's dozen dependent barrier steps took 12 us, the two
+// launches 6-7 us less (the top-k + permutation work-group of small decode
+// batches still takes up to kFusedPairs).
+constexpr int kOneGroupPairs = kFusedWaves * 64;
 
 template <int PPL>
 __device__ void permute_block(
@@ -311,7 +317,7 @@ __device__ void permute_block(
   }
 }
 
-// Mid-size batches (kFusedPairs < T * k <= kChunkedPairs, E + n_shared <=
+// Mid-size batches (kOneGroupPairs < T * k <= kChunkedPairs, E + n_shared <=
 // 256): two launches of one 256-thread work-group per kWgChunk positions.
 // The first counts each chunk's experts; the second has every work-group sum
 // the chunk counts itself (totals, and the prefix over earlier chunks), so no
@@ -538,7 +544,7 @@ extern "C" int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
   const int key_bits = key_bits_for(E);
   hipStream_t s = as_stream(stream);
   const int max_tiles = moeq_max_tiles(T, top_k, E, n_shared, bm);
-  if (T * top_k > kFusedPairs && T * top_k <= kChunkedPairs && E + n_shared <= kFusedExperts) {
+  if (T * top_k > kOneGroupPairs && T * top_k <= kChunkedPairs && E + n_shared <= kFusedExperts) {
     int32_t *cc = static_cast<int32_t *>(ws);
     const int nchunks = int(cdiv(T * top_k, kWgChunk));
     chunk_hist_kernel<<<nchunks, 256, 0, s>>>(idx, T, top_k, E, cc);
@@ -548,12 +554,9 @@ extern "C" int moeq_permute(const int32_t *idx, int64_t T, int top_k, int E,
                                                  counts, offsets, row_token, row_pair, inv_perm, tiles, n_tiles);
     return check_launch("permute/chunk_scatter");
   }
-  if (T * top_k <= kFusedPairs && E + n_shared <= kFusedExperts) {
-#define MOEQ_PF(Q)                                                                                       \
-  permute_fused_kernel<Q><<<1, 1024, 0, s>>>(idx, T, top_k, E, n_shared, bm, max_tiles, key_bits, counts, \
-                                             offsets, row_token, row_pair, inv_perm, tiles, n_tiles)
-    if (fused_ppl(T * top_k) == 1) MOEQ_PF(1); else MOEQ_PF(4);
-#undef MOEQ_PF
+  if (T * top_k <= kOneGroupPairs && E + n_shared <= kFusedExperts) {
+    permute_fused_kernel<1><<<1, 1024, 0, s>>>(idx, T, top_k, E, n_shared, bm, max_tiles, key_bits, counts,
+                                               offsets, row_token, row_pair, inv_perm, tiles, n_tiles);
     return check_launch("permute/fused");
   }
   int32_t *cc = static_cast<int32_t *>(ws);

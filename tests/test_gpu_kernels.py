@@ -95,7 +95,8 @@ def test_route_bias_and_ties(device):
 @pytest.mark.parametrize("T,k,E,S,bm", [(1, 8, 64, 0, 16), (1, 6, 64, 2, 16), (700, 2, 8, 0, 64),
                                         (2048, 8, 64, 0, 128), (4096, 8, 128, 0, 128),
                                         (300, 6, 64, 2, 32), (5000, 1, 3, 0, 128), (5000, 8, 64, 2, 128),
-                                        (9000, 8, 64, 0, 128), (3000, 4, 300, 0, 64)])
+                                        (9000, 8, 64, 0, 128), (3000, 4, 300, 0, 64),
+                                        (128, 8, 64, 0, 64), (129, 8, 64, 0, 64), (512, 8, 64, 0, 64)])
 def test_permute_bit_exact(device, T, k, E, S, bm):
     from robustgemq_amd import ops
     _say(f"[permute] T={T} k={k} E={E} shared={S} bm={bm}")
