@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-mixtral", action="store_true", help="skip the Mixtral-shaped decode and stack lines")
-    ap.add_argument("--no-others", action="store_true", help="skip the Qwen3 and DeepSeek prefill lines")
+    ap.add_argument("--no-others", action="store_true", help="skip the OLMoE 2-bit T=128, Qwen3 and DeepSeek prefill lines")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 256 MiB device-to-device copy first (reference size for HBM counters)")
@@ -259,8 +259,8 @@ def main():
         del mlayer
         torch.cuda.empty_cache()
     if not args.no_others:
-        # configs[2] and configs[3] at their prefill sizes
-        for name in ("qwen3_mixed", "deepseek_v2_lite"):
+        # configs[0], configs[2] and configs[3] at their prefill sizes
+        for name in ("olmoe_2bit", "qwen3_mixed", "deepseek_v2_lite"):
             if name == args.config:
                 continue
             ocfg = CONFIGS[name]

@@ -47,6 +47,13 @@ static Plan make_plan(const moeq_moe *m, int64_t T) {
   p.rows = p.pairs + int64_t(m->n_shared) * T;
   const double avg = double(p.pairs) / double(m->n_experts);
   p.bm = avg <= 16 ? 16 : avg <= 32 ? 32 : avg <= 64 ? 64 : 128;
+  // From 10 rows per expert many experts need a second 16-row tile, which
+  // streams their weights again; the 48-row class streams each expert once
+  // and wins when its down launch still has a work-group per CU (OLMoE
+  // T = 128: 64 experts x 8 column tiles, 1.04 -> 1.64 M tokens/s).  Few
+  // large experts keep the 16-row kernel's K split and deeper fetch ring
+  // (Mixtral B = 64 has 8 x 16 and was 9% slower in the 48-row class).
+  if (p.bm == 16 && avg > 10 && std::min<int64_t>(m->n_experts, p.pairs) * cdiv(m->hidden, 256) >= 256) p.bm = 32;
   p.max_tiles = moeq_max_tiles(T, m->top_k, m->n_experts, m->n_shared, p.bm);
   // 16-row (decode) down projections with few blocks also split K over
   // work-groups (fp32 slices the combine adds in order), so enough waves keep

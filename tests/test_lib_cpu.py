@@ -184,6 +184,14 @@ def test_layer_plan_and_workspace():
     assert plan[0] == 128 and plan[1] == 1
     assert lib.moeq_moe_plan(m, 1, plan) == 0
     assert plan[0] == 16 and plan[1] >= 1
+    # 16 rows per expert: 64 small experts take the 48-row class (each expert's
+    # weights streamed once), 8 large ones (Mixtral) keep the 16-row kernel
+    assert lib.moeq_moe_plan(m, 128, plan) == 0 and plan[0] == 32
+    assert lib.moeq_moe_plan(m, 64, plan) == 0 and plan[0] == 16
+    mx = L.MoeqMoe(hidden=4096, inter=14336, n_experts=8, top_k=2, n_shared=0, act_dtype=L.BF16,
+                   gate_dtype=L.BF16, norm_topk=1, gate_w=f, w1=_proj(4096, 14336), w3=_proj(4096, 14336),
+                   w2=_proj(14336, 4096), logit_bias=None)
+    assert lib.moeq_moe_plan(mx, 64, plan) == 0 and plan[0] == 16
     ws = lib.moeq_moe_workspace_size(m, 2048)
     # at least h [T*k, F] fp16 and y [T*k, H] fp16
     assert ws >= 2048 * 8 * (1024 + 2048) * 2
