@@ -149,7 +149,7 @@ int moeq_route_from_logits(const void *logits, int dtype, int64_t T, int E,
  * gemq/inference/moe_block.py:803-810 (also :256-262, :562-570, :1033-1040). */
 int moeq_max_tiles(int64_t T, int top_k, int E, int n_shared, int bm);
 /* Most rows one tile of tile class bm holds (the schedule's split size and
- * the grouped GEMM's row capacity): 16 -> 16, 32 -> 48, 64 -> 96,
+ * the grouped GEMM's row capacity): 16 -> 32, 32 -> 48, 64 -> 96,
  * 128 -> 160, 256 -> 256; 0 for any other bm.  No reference counterpart. */
 int moeq_tile_rows(int bm);
 size_t moeq_permute_workspace_size(int64_t T, int top_k, int E, int n_shared);

@@ -30,11 +30,11 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 // above their nominal height (an expert a little past 2 x 128 rows still
 // takes two tiles, not three).  0 for an unknown class.
 __host__ __device__ constexpr int tile_rows(int bm) {
-  return bm == 16 ? 16 : bm == 32 ? 48 : bm == 64 ? 96 : bm == 128 ? 160 : bm == 256 ? 256 : 0;
+  return bm == 16 ? 32 : bm == 32 ? 48 : bm == 64 ? 96 : bm == 128 ? 160 : bm == 256 ? 256 : 0;
 }
 
 // The grouped GEMM instantiates, per class, kernel variants for 16-row block
-// counts {1} (bm 16), {2, 3} (32), {2, 4, 6} (64), {2, 4, 8, 10} (128) and
+// counts {1, 2} (bm 16), {2, 3} (32), {2, 4, 6} (64), {2, 4, 8, 10} (128) and
 // {2, 4, 8, 16} (256); a tile of b blocks runs the smallest count >= b.  The
 // schedule cuts experts into tiles of the largest count and of the one below
 // it, returned here.

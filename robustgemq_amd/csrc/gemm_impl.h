@@ -229,38 +229,52 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
     // of them at once, a longer one keeps a 4-chunk ring in flight.  Steps
     // past a wave's last chunk re-read a valid chunk and multiply it by a
     // zero A fragment, so every fetch and MFMA is unconditional (no joins for
-    // the wait counts to merge).
+    // the wait counts to merge).  A tile of two 16-row blocks (MBA = 2: an
+    // expert with 17..32 rows, one pass over its weights instead of two)
+    // fetches both blocks' fragments and keeps to the ring past 4 chunks.
     constexpr int AES = 2;
-    const int rr = row0 + min(l16, mcount - 1);
-    const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
-    const char *arow = abytes + src * g.lda * AES;
+    const char *arow[MBA];
+#pragma unroll
+    for (int mb = 0; mb < MBA; ++mb) {
+      const int rr = row0 + min(16 * mb + l16, mcount - 1);
+      const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
+      arow[mb] = abytes + src * g.lda * AES;
+    }
     const int cfirst = KS ? c0 + wave : c0, cstep = KS ? NW : 1;
     const int nc = KS ? (c1 > c0 + wave ? (c1 - c0 - wave + NW - 1) / NW : 0) : max(c1 - c0, 0);
-    auto fetch = [&](int j, uint4 (&av)[4], uint32_t (&w)[NP][NB][BITS], uint32_t (&sz)[NP][NB]) {
+    auto fetch = [&](int j, uint4 (&av)[MBA][4], uint32_t (&w)[NP][NB][BITS], uint32_t (&sz)[NP][NB]) {
       // a K-split wave with no chunk of its own (fewer chunks than waves, or
       // an empty split) still fetches a valid chunk, c1 - 1, times zero
       const int c = max(min(cfirst + cstep * min(j, max(nc - 1, 0)), c1 - 1), 0);
-      const uint4 *pa = reinterpret_cast<const uint4 *>(arow + (int64_t(c) * 128 + 32 * kb) * AES);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) av[t] = pa[t];
+      for (int mb = 0; mb < MBA; ++mb) {
+        const uint4 *pa = reinterpret_cast<const uint4 *>(arow[mb] + (int64_t(c) * 128 + 32 * kb) * AES);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) av[mb][t] = pa[t];
+      }
       load_b(c, w, sz);
     };
-    auto step = [&](bool live, const uint4 (&av)[4], const uint32_t (&w)[NP][NB][BITS], const uint32_t (&sz)[NP][NB]) {
+    auto step = [&](bool live, const uint4 (&av)[MBA][4], const uint32_t (&w)[NP][NB][BITS],
+                    const uint32_t (&sz)[NP][NB]) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const f16x8 A = live ? to_f16x8<ADT>(av[t]) : f16x8{};
+        f16x8 A[MBA];
+#pragma unroll
+        for (int mb = 0; mb < MBA; ++mb) A[mb] = live ? to_f16x8<ADT>(av[mb][t]) : f16x8{};
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             const f16x8 B = deq_frag<BITS, DQ>(w[p][nb], sz[p][nb], t);
-            acc[p][0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[p][0][nb], 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < MBA; ++mb)
+              acc[p][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb], B, acc[p][mb][nb], 0, 0, 0);
           }
       }
     };
     auto all_at_once = [&](auto slots) {
       constexpr int S = decltype(slots)::value;
-      uint4 ar[S][4];
+      uint4 ar[S][MBA][4];
       uint32_t wr[S][NP][NB][BITS], sr[S][NP][NB];
 #pragma unroll
       for (int j = 0; j < S; ++j) fetch(j, ar[j], wr[j], sr[j]);
@@ -273,11 +287,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
       all_at_once(std::integral_constant<int, 2>{});
     } else if (nc > 2 && nc <= 4) {
       all_at_once(std::integral_constant<int, 4>{});
-    } else if (nc > 4 && nc <= 8) {
+    } else if (MBA == 1 && nc > 4 && nc <= 8) {
       all_at_once(std::integral_constant<int, 8>{});
-    } else if (nc > 8) {
+    } else if (nc > 4) {
       constexpr int DEPTH = 4;
-      uint4 ar[DEPTH][4];
+      uint4 ar[DEPTH][MBA][4];
       uint32_t wr[DEPTH][NP][NB][BITS], sr[DEPTH][NP][NB];
 #pragma unroll
       for (int d = 0; d < DEPTH - 1; ++d) fetch(d, ar[d], wr[d], sr[d]);
@@ -293,13 +307,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
     // KS: partial sums of the NW waves -> wave 0, added in wave order
     if constexpr (KS) {
       float *red = reinterpret_cast<float *>(&As0[0][0]);
+      static_assert((NW - 1) * NP * MBA * NB * 4 * 64 * 4 <= 48 * 16 * 16, "K-split partials exceed As0");
       if (wave > 0) {
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
+          for (int mb = 0; mb < MBA; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[(((wave - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane] = acc[p][0][nb][i];
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                red[((((wave - 1) * NP + p) * MBA + mb) * NB * 4 + nb * 4 + i) * 64 + lane] = acc[p][mb][nb][i];
       }
       __syncthreads();
       if (wave > 0) return;
@@ -308,9 +326,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
+          for (int mb = 0; mb < MBA; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[p][0][nb][i] += red[(((w - 1) * NP + p) * NB * 4 + nb * 4 + i) * 64 + lane];
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                acc[p][mb][nb][i] += red[((((w - 1) * NP + p) * MBA + mb) * NB * 4 + nb * 4 + i) * 64 + lane];
     }
   } else {
     // ---------------- prefill shapes: A copied global -> LDS, double buffered
@@ -427,7 +448,7 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
   const int mb_act = (mcount + 15) >> 4;
 #define MOEQ_T(M) gemm_tile<BM, NW, NB, NP, EPI, ADT, ODT, BITS, DQ, M, KS>(g, e, row0, mcount, nt, c0, c1, As0, As1)
   if constexpr (BM == 16) {
-    MOEQ_T(1);
+    if (mb_act <= 1) MOEQ_T(1); else MOEQ_T(2);
   } else if constexpr (BM == 32) {
     if (mb_act <= 2) MOEQ_T(2); else MOEQ_T(3);
   } else if constexpr (BM == 64) {
@@ -468,8 +489,8 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
   }
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
-  // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * NB * 4
-  // floats per lane, at most 12 KB.  The prefill classes hold tile_rows(BM)
+  // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * MBA *
+  // NB * 4 floats per lane, at most 12 KB.  The prefill classes hold tile_rows(BM)
   // rows per buffer (two 40 KB buffers for the 160-row class: two
   // work-groups fill the 160 KB of LDS).
   __shared__ uint4 As0[BM == 16 ? 48 : tile_rows(BM)][16];

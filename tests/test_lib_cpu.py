@@ -142,7 +142,7 @@ def test_max_tiles_bounds_every_routing():
 
 def test_tile_rows_classes():
     lib = L.lib()
-    assert [lib.moeq_tile_rows(b) for b in (16, 32, 64, 128, 256)] == [16, 48, 96, 160, 256]
+    assert [lib.moeq_tile_rows(b) for b in (16, 32, 64, 128, 256)] == [32, 48, 96, 160, 256]
     assert lib.moeq_tile_rows(48) == 0 and lib.moeq_tile_rows(0) == 0
 
 
@@ -151,7 +151,7 @@ def test_tile_split_rule():
     rows at 16-row boundaries, and never run more 16-row blocks (rounded up to
     the kernel's variants) than an even split of the rows would."""
     from robustgemq_amd.linear import split_rows
-    variants = {16: (1,), 32: (2, 3), 64: (2, 4, 6), 128: (2, 4, 8, 10), 256: (2, 4, 8, 16)}
+    variants = {16: (1, 2), 32: (2, 3), 64: (2, 4, 6), 128: (2, 4, 8, 10), 256: (2, 4, 8, 16)}
 
     def run_blocks(rows, bm):
         b = -(-rows // 16)
