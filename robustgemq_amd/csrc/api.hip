@@ -4,6 +4,7 @@
 
 #include <algorithm>
 
+#include "gemm_impl.h"
 #include "routing.h"
 
 extern "C" int moeq_gemm_tile_n(int bm, int epilogue);
@@ -241,7 +242,9 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   gu.splits = 1;
   gu.split_stride = 0;
   if (ev0 && (rc = hip_ok(hipEventRecord(ev0, as_stream(stream)), "moe: event record"))) return rc;
-  rc = moeq_grouped_gemm(&gu, &m->w1, &m->w3, stream);
+  // a token picks an expert at most once: no tile holds more than T rows
+  const int max_rows = int(std::min<int64_t>(T, tile_rows(p.bm)));
+  rc = grouped_gemm_rows(&gu, &m->w1, &m->w3, max_rows, stream);
   if (rc) return rc;
   if (ev1 && (rc = hip_ok(hipEventRecord(ev1, as_stream(stream)), "moe: event record"))) return rc;
 
@@ -256,7 +259,7 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   dn.ldo = m->hidden;
   dn.splits = p.splits;
   dn.split_stride = p.rows * m->hidden;
-  rc = moeq_grouped_gemm(&dn, &m->w2, nullptr, stream);
+  rc = grouped_gemm_rows(&dn, &m->w2, nullptr, max_rows, stream);
   if (rc) return rc;
 
   return moeq_combine(at(p.off_y), p.y_dtype, p.splits, p.rows * m->hidden, m->hidden, inv, w, T,

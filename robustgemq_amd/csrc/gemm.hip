@@ -22,8 +22,8 @@ static int check_proj(const moeq_proj *p, const char *name) {
   return MOEQ_OK;
 }
 
-extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
-                                 const moeq_proj *p1, void *stream) {
+int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows,
+                            void *stream) {
   if (!gm) return fail(MOEQ_ERR_INVALID, "grouped_gemm: null descriptor");
   if (!gm->a || !gm->tiles || !gm->n_tiles || !gm->out) return fail(MOEQ_ERR_INVALID, "grouped_gemm: null pointer");
   int rc = check_proj(p0, "p0");
@@ -66,6 +66,7 @@ extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
   g.split_stride = gm->split_stride;
   g.nchunks = nchunks;
   g.chunks_per_split = int(cdiv(nchunks, gm->splits));
+  g.max_rows = max_rows;
   hipStream_t s = as_stream(stream);
   const int mt = gm->max_tiles, sp = gm->splits;
   const bool silu = gm->epilogue == MOEQ_EPI_SILU_MUL;
@@ -77,6 +78,11 @@ extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
     case 256: return launch_grouped_gemm<256>(g, silu, gm->a_dtype, gm->out_dtype, mt, sp, s);
     default: return fail(MOEQ_ERR_INVALID, "grouped_gemm: bm=%d not in {16, 32, 64, 128, 256}", gm->bm);
   }
+}
+
+extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
+                                 const moeq_proj *p1, void *stream) {
+  return grouped_gemm_rows(gm, p0, p1, 0, stream);
 }
 
 // Column tile width the kernels use for a given (bm, epilogue); the layer

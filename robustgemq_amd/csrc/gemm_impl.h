@@ -49,6 +49,9 @@ struct GemmArgs {
   void *out;
   int64_t ldo, split_stride;
   int n_ntiles, nchunks, chunks_per_split;
+  // most rows any tile of this launch can hold (0: the class capacity);
+  // 16-row launches at most 16 run the kernel without the two-block path
+  int max_rows;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -442,13 +445,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
   }
 }
 
-template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, bool KS>
+template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, bool KS, bool MB2>
 __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0, int mcount, int nt, int c0,
                                               int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {
   const int mb_act = (mcount + 15) >> 4;
 #define MOEQ_T(M) gemm_tile<BM, NW, NB, NP, EPI, ADT, ODT, BITS, DQ, M, KS>(g, e, row0, mcount, nt, c0, c1, As0, As1)
   if constexpr (BM == 16) {
-    if (mb_act <= 1) MOEQ_T(1); else MOEQ_T(2);
+    if constexpr (MB2) {
+      if (mb_act <= 1) MOEQ_T(1); else MOEQ_T(2);
+    } else {
+      MOEQ_T(1);
+    }
   } else if constexpr (BM == 32) {
     if (mb_act <= 2) MOEQ_T(2); else MOEQ_T(3);
   } else if constexpr (BM == 64) {
@@ -464,7 +471,7 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
 // Two work-groups per CU for the 32..128 classes (tiles of up to 48..160
 // rows) and one 8-wave group for the 256-row shape (its two A buffers take
 // 128 KB of LDS): 2 waves per SIMD.
-template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, bool KS>
+template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, bool KS, bool MB2 = true>
 __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
   // The grid is sized for the host-side bound on row tiles; blocks past the
   // real count (read from the device schedule) exit together.  Work-groups
@@ -501,7 +508,7 @@ __global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grou
   const int c1 = min(c0 + g.chunks_per_split, g.nchunks);
   const int bits = g.p[0].nbits[e];
   const int dq = g.dq_mode;
-#define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D, KS>(g, e, row0, mcount, nt, c0, c1, As0, As1)
+#define MOEQ_TILE(B, D) gemm_tile_mba<BM, NW, NB, NP, EPI, ADT, ODT, B, D, KS, MB2>(g, e, row0, mcount, nt, c0, c1, As0, As1)
 #define MOEQ_BITS(B)                                                   \
   if (dq == MOEQ_DQ_HQQ_INT) MOEQ_TILE(B, MOEQ_DQ_HQQ_INT);           \
   else if (dq == MOEQ_DQ_HQQ) MOEQ_TILE(B, MOEQ_DQ_HQQ);              \
@@ -536,12 +543,17 @@ template <> struct Shape<128, false> { static constexpr int NW = 4, NB = 4; };
 template <> struct Shape<256, true> { static constexpr int NW = 8, NB = 1; };
 template <> struct Shape<256, false> { static constexpr int NW = 8, NB = 2; };
 
+// moeq_grouped_gemm for callers that know the most rows any tile holds
+// (max_rows > 0; the layer forward: at most T per expert), which lets 16-row
+// launches of at most 16 rows per tile skip the two-block kernel path.
+int grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, void *stream);
+
 // Launches one configuration (defined in gemm_bm<BM>.hip).
 template <int BM>
 int launch_grouped_gemm(const GemmArgs &g, bool silu, int a_dtype, int out_dtype, int max_tiles, int splits,
                         hipStream_t s);
 
-template <int BM, bool SILU, int ADT, int ODT, bool KS = false>
+template <int BM, bool SILU, int ADT, int ODT, bool KS = false, bool MB2 = true>
 inline int launch_one(const GemmArgs &g0, int max_tiles, int splits, hipStream_t s) {
   using S = Shape<BM, SILU>;
   static_assert(!KS || BM == 16, "K split over waves is a 16-row block variant");
@@ -550,7 +562,7 @@ inline int launch_one(const GemmArgs &g0, int max_tiles, int splits, hipStream_t
   const int64_t blocks = int64_t(max_tiles) * g.n_ntiles;
   if (blocks > 0x7fffffff) return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: grid too large");
   dim3 grid(unsigned(blocks), 1, unsigned(splits)), block(S::NW * 64);
-  grouped_gemm_kernel<BM, S::NW, S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ADT, ODT, KS>
+  grouped_gemm_kernel<BM, S::NW, S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ADT, ODT, KS, MB2>
       <<<grid, block, 0, s>>>(g);
   return check_launch("grouped_gemm");
 }
