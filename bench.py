@@ -276,6 +276,14 @@ def main():
                 runs[f"{name}_prefill_T{tp}"] = {"tokens_per_s": round(tp / (ms * 1e-3), 1), "ms": round(ms, 4),
                                                  "layer_tflops": round(tf, 1),
                                                  "mfma_frac_layer": round(tf / PEAK_MFMA_F16_TFLOPS, 4)}
+            if ocfg.runs.get("decode") and not args.no_decode:
+                # a second layer (seed 1): two layers' experts exceed the
+                # last-level cache, so the decode stack streams them from HBM
+                ow2 = make_weights(ocfg, seed=1, quant_device=dev)
+                olayer2 = build_block(ocfg, ow2, device=dev)._layer
+                del ow2
+                runs.update(decode_runs(ocfg, [olayer, olayer2], ocfg.runs["decode"], args, stream, f"{name}_"))
+                del olayer2
             del olayer
             torch.cuda.empty_cache()
     extra["runs"] = runs
@@ -348,7 +356,8 @@ def decode_runs(cfg, layers, batches, args, stream, tag):
         def stack():
             h = xb
             for i, ly in enumerate(layers):
-                ly.forward(h, out=hs[i], want_logits=False)
+                # batch 1 is forward_one_token, as the reference decodes
+                ly.forward(h, out=hs[i], want_logits=False, one_token=B == 1)
                 h = hs[i]
 
         stack()  # sizes the workspaces before capture

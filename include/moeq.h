@@ -70,6 +70,13 @@ typedef struct moeq_moe {
   const void *gate_w; /* [n_experts, hidden] in gate_dtype                     */
   moeq_proj w1, w3, w2; /* gate_proj, up_proj, down_proj                       */
   const float *logit_bias; /* [n_experts] fp32 added to the logits, or NULL     */
+  /* Nonzero: a one-token forward (T == 1) routes as Mixtral's
+   * forward_one_token does (gemq/inference/moe_block.py:280-283): softmax
+   * probabilities rounded to act_dtype are ranked (equal values: lower expert
+   * index first) and renormalised in act_dtype, w = rnd(p / rnd(sum p)).
+   * Zero: every T ranks the logits with fp32 softmax weights (:245-249 and
+   * the other families).  Ignored for T > 1. */
+  int32_t one_token_act_softmax;
 } moeq_moe;
 
 const char *moeq_last_error(void);
@@ -185,8 +192,11 @@ typedef struct moeq_gemm {
 /* One launch over every row tile of every expert:
  * out[r, :] = epilogue(A[row_src[r], :] @ deq(W[expert(r)])).
  * p1 must be NULL for MOEQ_EPI_STORE and match p0's layout for SILU_MUL.
- * Every A row the tiles address (row_src[r], or r) must start below 2 GiB
- * from a (32-bit row offsets); one expert's packed words must be < 2 GiB.
+ * Every A row the tiles address (row_src[r], or r) must lie wholly within
+ * the first 2 GiB from a, i.e. (row + 1) * lda * element size <= 2^31
+ * (the LDS-staged tiles address rows with 32-bit offsets; the caller checks
+ * this, the library cannot see the rows row_src names); one expert's packed
+ * words must be < 2 GiB.
  * Replaces the per-expert launches of dequant_group_gemm_triton
  * (gemq/triton_kernels/dequant_group_gemm.py:155-202, called once per hit
  * expert at gemq/inference/moe_block.py:766-777), dequant_gemm_triton
@@ -207,6 +217,15 @@ int moeq_combine(const void *y, int y_dtype, int splits, int64_t split_stride,
                  int64_t ldy, const int32_t *inv_perm, const float *w,
                  int64_t T, int top_k, int n_shared, int H, void *out,
                  int out_dtype, void *stream);
+
+/* out[i] = fp16(silu(x1[i]) * x3[i]) for i < n, computed in fp32 from fp16
+ * x1 / x3 (the gate/up epilogue's arithmetic).  n % 8 == 0.
+ * Replaces the fp32 SiLU*mul prologue of fused_dequant_down_proj_triton,
+ * gemq/triton_kernels/fused_dequant_bmm.py:229-239 (and the eager
+ * F.silu(x1) * x3 of moe_block.py:775); the product then feeds
+ * moeq_grouped_gemm. */
+int moeq_silu_mul(const uint16_t *x1, const uint16_t *x3, int64_t n,
+                  uint16_t *out, void *stream);
 
 /* ------------------------------------------------------------- whole layer */
 

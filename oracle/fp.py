@@ -58,6 +58,21 @@ def round_to_bf16(a32):
     return bf16_bits_to_f32(to_bf16_bits(a32))
 
 
+def near_midpoint(a32, dtype, ulps=4):
+    """True where a positive fp32 value lies within `ulps` fp32 ulps of a
+    rounding midpoint of `dtype` ('f16' normal range | 'bf16'): there two fp32
+    evaluations of the same formula that differ in their last bits may round
+    to different neighbours."""
+    u = np.asarray(a32, dtype=np.float32).view(np.uint32).astype(np.int64)
+    if dtype == "bf16":
+        low, mid = u & 0xFFFF, 0x8000
+    elif dtype == "f16":
+        low, mid = u & 0x1FFF, 0x1000
+    else:
+        return np.zeros(u.shape, bool)
+    return np.abs(low - mid) <= ulps
+
+
 def round_to(a32, dtype):
     """Round fp32 values to the storage dtype name ('f16' | 'bf16' | 'f32'),
     returned as fp32 values."""

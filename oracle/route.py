@@ -12,7 +12,7 @@ import os
 
 import numpy as np
 
-from .fp import round_to
+from .fp import near_midpoint, round_to
 
 _LIB = None
 
@@ -70,6 +70,34 @@ def topk_route(logits32, top_k, norm_topk):
     if norm_topk:
         w = (w.astype(np.float64) / w.astype(np.float64).sum(axis=1, keepdims=True)).astype(np.float32)
     return idx, w
+
+
+def topk_route_act_softmax(logits32, top_k, dtype):
+    """Mixtral's forward_one_token router, moe_block.py:280-283:
+
+        expert_weights = F.softmax(scores, dim=-1)          # scores in `dtype`
+        expert_weights, expert_indices = torch.topk(expert_weights, top_k)
+        expert_weights /= expert_weights.sum(dim=-1, keepdim=True)
+
+    torch runs softmax on a 16-bit tensor in fp32 and rounds each output to
+    the tensor's type; topk ranks those rounded values (equal values: the
+    lower expert index first, the order the kernels use; CUDA's tie order is
+    not specified); the sum accumulates in fp32 and is rounded, and so is
+    each quotient.  dtype: 'f16' | 'bf16'.  Returns (idx int32 [T, k], w fp32
+    [T, k] holding `dtype` values, p fp32 [T, E] the rounded probabilities,
+    fragile bool [T] marking tokens with a probability within a few fp32 ulps
+    of a rounding midpoint of `dtype`: any fp32 softmax, torch's included,
+    may round those to the other neighbour)."""
+    lg = np.asarray(logits32, dtype=np.float32)
+    m = lg.max(axis=1, keepdims=True)
+    e = np.exp((lg - m).astype(np.float64))
+    p32 = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
+    p = round_to(p32, dtype)
+    idx = np.argsort(-p, axis=1, kind="stable")[:, :top_k].astype(np.int32)
+    sel = np.take_along_axis(p, idx.astype(np.int64), axis=1)
+    s = round_to(sel.sum(axis=1, keepdims=True, dtype=np.float32), dtype)
+    w = round_to((sel / s).astype(np.float32), dtype)
+    return idx, w, p, near_midpoint(p32, dtype).any(axis=1)
 
 
 def permute(idx, n_experts, n_shared=0):

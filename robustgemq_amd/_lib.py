@@ -54,6 +54,7 @@ class MoeqMoe(ctypes.Structure):
         ("w3", MoeqProj),
         ("w2", MoeqProj),
         ("logit_bias", c_void_p),
+        ("one_token_act_softmax", c_int32),
     ]
 
 
@@ -98,6 +99,7 @@ SIGNATURES = {
                                   ctypes.POINTER(MoeqProj), c_void_p]),
     "moeq_combine": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                              c_int, c_int, c_int, c_void_p, c_int, c_void_p]),
+    "moeq_silu_mul": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "moeq_moe_workspace_size": (c_size_t, [ctypes.POINTER(MoeqMoe), c_int64]),
     "moeq_moe_forward": (c_int, [ctypes.POINTER(MoeqMoe), c_void_p, c_int64, c_void_p, c_int,
                                  c_void_p, c_void_p, c_size_t, c_void_p]),

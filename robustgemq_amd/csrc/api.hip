@@ -183,8 +183,14 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
     RouteArgs r1 = ra;  // its logits stay in LDS unless asked for
     r1.logits = logits_out;
     r1.store_dtype = ldt;
+    // Mixtral's one-token router ranks and renormalises 16-bit probabilities
+    const bool act_softmax = T == 1 && m->one_token_act_softmax;
+    if (act_softmax) r1.prob_dtype = m->act_dtype;
     if (launch_route1(r1, po, s)) {
       if ((rc = check_launch("moe/route1"))) return rc;
+    } else if (act_softmax) {
+      return fail(MOEQ_ERR_UNSUPPORTED, "moe: one_token_act_softmax needs the one-token router "
+                  "(n_experts <= 256, top_k <= 16, hidden %% 8 == 0 and <= 4096)");
     } else {
       if ((rc = launch_route_logits(ra, s))) return rc;
       rc = launch_topk_permute(lg, lg_dt, T, m->n_experts, m->top_k, m->norm_topk ? 1 : 0, idx, w, m->n_shared,

@@ -176,3 +176,31 @@ extern "C" int moeq_combine(const void *y, int y_dtype, int splits, int64_t spli
                              out_dtype);
   return check_launch("combine");
 }
+
+// ------------------------------------------------------------- SiLU * mul
+// out = fp16(silu(x1) * x3), 8 elements per thread, fp32 arithmetic shared
+// with the gate/up epilogue (silu_mul in common.h).
+__global__ void silu_mul_kernel(const uint16_t *x1, const uint16_t *x3, int64_t n, uint16_t *out) {
+  const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;  // n is a multiple of 8
+  const uint4 a = *reinterpret_cast<const uint4 *>(x1 + i);
+  const uint4 b = *reinterpret_cast<const uint4 *>(x3 + i);
+  const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = silu_mul(f16_bits_to_f32(uint16_t(wa[j] & 0xffffu)), f16_bits_to_f32(uint16_t(wb[j] & 0xffffu)));
+    const float hi = silu_mul(f16_bits_to_f32(uint16_t(wa[j] >> 16)), f16_bits_to_f32(uint16_t(wb[j] >> 16)));
+    o[j] = uint32_t(f32_to_f16_bits(lo)) | (uint32_t(f32_to_f16_bits(hi)) << 16);
+  }
+  *reinterpret_cast<uint4 *>(out + i) = (uint4){o[0], o[1], o[2], o[3]};
+}
+
+extern "C" int moeq_silu_mul(const uint16_t *x1, const uint16_t *x3, int64_t n, uint16_t *out, void *stream) {
+  if (!x1 || !x3 || !out) return fail(MOEQ_ERR_INVALID, "silu_mul: null pointer");
+  if (n <= 0 || n % 8) return fail(MOEQ_ERR_INVALID, "silu_mul: n=%lld must be a positive multiple of 8", (long long)n);
+  const int64_t blocks = cdiv(n / 8, 256);
+  if (blocks > 0x7fffffff) return fail(MOEQ_ERR_UNSUPPORTED, "silu_mul: n=%lld too large", (long long)n);
+  silu_mul_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, as_stream(stream)>>>(x1, x3, n, out);
+  return check_launch("silu_mul");
+}

@@ -72,4 +72,9 @@ __device__ __forceinline__ float load_as_f32(const void *p, int dtype, int64_t i
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// silu(g) * u in fp32: the gate/up epilogue and moeq_silu_mul share it.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 }  // namespace moeq

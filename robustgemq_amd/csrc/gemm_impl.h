@@ -150,10 +150,6 @@ __device__ __forceinline__ f16x8 to_f16x8(uint4 u) {
   }
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-}
-
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, int BITS, int DQ, int MBA, bool KS>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, int mcount, int nt,
                                           int c0, int c1, uint4 (*As0)[16], uint4 (*As1)[16]) {

@@ -367,7 +367,7 @@ __global__ __launch_bounds__(kR1Waves * 64) void route1_kernel(RouteArgs a, Perm
     float wsel[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) vals[r] = 64 * r + lane < E ? lg[64 * r + lane] : -INFINITY;
-    topk_ranks<R>(vals, E, k, a.norm, rank, wsel);
+    topk_ranks<R>(vals, E, k, a.norm, rank, wsel, a.prob_dtype);
     int before = 0;  // selected experts in earlier registers
 #pragma unroll
     for (int r = 0; r < R; ++r) {

@@ -25,6 +25,11 @@ struct RouteArgs {
   int32_t *idx;
   float *w;
   uint16_t *x16 = nullptr;  // optional [T, H] fp16 copy of x, written by the expert-0 waves
+  // MOEQ_F32: rank the logits, fp32 softmax weights (every family's
+  // forward_n_tokens).  MOEQ_F16 / MOEQ_BF16: softmax probabilities rounded
+  // to that type are ranked and renormalised in it (Mixtral's
+  // forward_one_token); only the one-token kernel (route1) honours it.
+  int prob_dtype = MOEQ_F32;
 };
 
 __device__ __forceinline__ float round_logit(float v, int dtype) {
@@ -74,14 +79,38 @@ __device__ __forceinline__ void load8(const void *p, int dtype, int64_t i, float
 // directly: every value is broadcast once (v_readlane) and compared with all
 // of them, so there is no sequential select-and-remove loop and no
 // dynamically indexed register.
+//
+// prob_dtype F16 / BF16 restates a router that runs softmax on a 16-bit
+// tensor (F.softmax computes in fp32 and rounds its output), ranks those
+// rounded probabilities with torch.topk and renormalises in the same type
+// (gemq/inference/moe_block.py:280-283): p = rnd(exp(l - max) / sum),
+// ranked by p (equal p: lower index first), w = rnd(p / rnd(sum_sel p)).
+// The selected sum is exact in fp32 for k = 2 (two 16-bit values), so its
+// order does not matter there.
 template <int EREG>
 __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&rank)[EREG],
-                           float (&wsel)[EREG]) {
+                           float (&wsel)[EREG], int prob_dtype = MOEQ_F32) {
   const int lane = lane_id();
 #pragma unroll
   for (int r = 0; r < EREG; ++r) {
     const int e = 64 * r + lane;
     if (e >= E || vals[r] != vals[r]) vals[r] = -INFINITY;  // NaN ranks last
+  }
+  if (prob_dtype != MOEQ_F32) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < EREG; ++r) mx = fmaxf(mx, vals[r]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float den = 0.f;
+#pragma unroll
+    for (int r = 0; r < EREG; ++r)
+      if (64 * r + lane < E) den += expf(vals[r] - mx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o);
+#pragma unroll
+    for (int r = 0; r < EREG; ++r)
+      vals[r] = 64 * r + lane < E ? round_logit(expf(vals[r] - mx) / den, prob_dtype) : -INFINITY;
   }
 #pragma unroll
   for (int r = 0; r < EREG; ++r) rank[r] = 0;
@@ -100,6 +129,18 @@ __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&ra
         rank[r] += (v > vals[r] || (v == vals[r] && e2 < e)) ? 1 : 0;
       }
     }
+  }
+  if (prob_dtype != MOEQ_F32) {
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < EREG; ++r)
+      if (64 * r + lane < E && rank[r] < k) psum += vals[r];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) psum += __shfl_xor(psum, o);
+    const float s = round_logit(psum, prob_dtype);
+#pragma unroll
+    for (int r = 0; r < EREG; ++r) wsel[r] = norm ? round_logit(vals[r] / s, prob_dtype) : vals[r];
+    return;
   }
   // m is the top value (sel 0) unless every logit is -inf / NaN
   float den = 0.f;

@@ -118,6 +118,11 @@ class QuantLinear(nn.Module):
                                 torch.tensor([nt], dtype=torch.int32, device=dev), nt)
         return self._tiles[key]
 
+    def _gemm(self, x2):
+        M = x2.shape[0]
+        bm, tiles, n, nt = self._tile_list(M, x2.device)
+        return ops.grouped_gemm(x2, M, self.out_features, tiles, n, nt, bm, self._proj)
+
     def forward(self, x):
         K = self.in_features
         assert x.shape[-1] == K, (x.shape, K)
@@ -129,8 +134,13 @@ class QuantLinear(nn.Module):
         M = x2.shape[0]
         if M == 0:
             return x.new_empty((*lead, self.out_features))
-        bm, tiles, n, nt = self._tile_list(M, x2.device)
-        y = ops.grouped_gemm(x2, M, self.out_features, tiles, n, nt, bm, self._proj)
+        # LDS-staged tiles address rows with 32-bit offsets: run the rows in
+        # slices that each stay within 2 GiB
+        rows_max = max(16, (ops.A_ROWS_MAX_BYTES // (K * 2)) // 16 * 16)
+        if M > rows_max:
+            y = torch.cat([self._gemm(x2[r:r + rows_max]) for r in range(0, M, rows_max)])
+        else:
+            y = self._gemm(x2)
         y = y.to(x2.dtype)
         if self.bias is not None:
             y = y + self.bias.to(y.dtype)

@@ -115,6 +115,7 @@ class _QuantFusedMoEBase(nn.Module):
 
     _proj_names = ("gate_proj", "up_proj", "down_proj")  # -> w1, w3, w2
     _always_renorm = False
+    _one_token_act_softmax = False  # Mixtral: 16-bit softmax in forward_one_token
     _gate_fp32 = False
     _returns_logits = True
     _family = "?"
@@ -147,7 +148,8 @@ class _QuantFusedMoEBase(nn.Module):
         check_w1_w3_aligned(self)
         gate_w = self.gate.weight.data.float() if self._gate_fp32 else self.gate.weight.data.to(act_dtype)
         n_shared = shared if shared else 0
-        self._layer = MoELayer(gate_w, w1, w3, w2, self.top_k, self._renorm(), act_dtype, n_shared=n_shared)
+        self._layer = MoELayer(gate_w, w1, w3, w2, self.top_k, self._renorm(), act_dtype, n_shared=n_shared,
+                               one_token_act_softmax=self._one_token_act_softmax)
         return self
 
     def _renorm(self):
@@ -209,12 +211,12 @@ class _QuantFusedMoEBase(nn.Module):
         return None
 
     # -- forward ----------------------------------------------------------
-    def _run(self, hidden_states, want_logits):
+    def _run(self, hidden_states, want_logits, one_token=False):
         if self._layer is None:
             raise RuntimeError("block has no weights: build it with from_hf() or from_quantized()")
         B, S, H = hidden_states.shape
         x = hidden_states.reshape(-1, H)
-        out, logits = self._layer.forward(x, want_logits=want_logits)
+        out, logits = self._layer.forward(x, want_logits=want_logits, one_token=one_token)
         return out.reshape(B, S, H), logits
 
     def forward_n_tokens(self, hidden_states):
@@ -227,7 +229,7 @@ class _QuantFusedMoEBase(nn.Module):
         """Single-token decode (moe_block.py:817-853); capture-safe."""
         B, S, H = hidden_states.shape
         assert B * S == 1, f"This function only supports single token forward. But got {B * S} tokens."
-        out, _ = self._run(hidden_states, want_logits=False)
+        out, _ = self._run(hidden_states, want_logits=False, one_token=True)
         return (out, None) if self._returns_logits else out
 
     def forward(self, hidden_states):
@@ -265,6 +267,9 @@ class QuantFusedMixtralMoEBlock(_QuantFusedMoEBase):
     _family = "MixtralSparseMoeBlock"
     _proj_names = ("w1", "w3", "w2")
     _always_renorm = True
+    # forward_one_token ranks and renormalises softmax probabilities in the
+    # activation dtype (moe_block.py:280-283), forward_n_tokens in fp32 (:245-249)
+    _one_token_act_softmax = True
 
     def _init_dims(self, config):
         self.hidden_dim = config.hidden_size

@@ -16,8 +16,9 @@ All launches go to torch's current stream; outputs are allocated with torch
 repacking of reference-layout tensors handed to the kernel-level operators.
 """
 
+import weakref
+
 import torch
-import torch.nn.functional as F
 
 from . import _lib as L
 from .experts import QuantProjection, pack_codes, unpack_words
@@ -84,6 +85,17 @@ def permute(idx, n_experts, n_shared=0, bm=16):
 
 
 # ------------------------------------------------------------- expert GEMMs
+# Row tiles of 32 rows and more stage A through LDS with 32-bit byte offsets:
+# every row they read must end within the first 2 GiB of `a`.
+A_ROWS_MAX_BYTES = 1 << 31
+
+
+def a_rows_addressable(a, bm):
+    """True when every row of `a` can feed a tile of class bm: 16-row tiles
+    load rows with 64-bit addresses, larger ones need the rows within 2 GiB."""
+    return bm < 32 or a.shape[0] * a.stride(0) * a.element_size() <= A_ROWS_MAX_BYTES
+
+
 def grouped_gemm(a, rows, n_out, tiles, n_tiles, max_tiles, bm, p0, p1=None, row_src=None,
                  out_dtype=torch.float16, splits=1):
     """One launch over all row tiles: out[r] = A[row_src[r]] @ deq(W[expert(r)])
@@ -93,6 +105,9 @@ def grouped_gemm(a, rows, n_out, tiles, n_tiles, max_tiles, bm, p0, p1=None, row
     N = p0.N
     if a.dtype == torch.bfloat16 and bm >= 32:
         a = a.to(torch.float16)  # LDS-staged tiles read F16 rows (exact for |x| in fp16 range)
+    if not a_rows_addressable(a, bm):
+        raise ValueError(f"grouped_gemm: activations of {a.shape[0]} rows x {a.stride(0)} elements exceed "
+                         f"{A_ROWS_MAX_BYTES} bytes (split the rows, as QuantLinear.forward does)")
     epi = L.EPI_SILU_MUL if p1 is not None else L.EPI_STORE
     shape = (rows, N) if splits == 1 else (splits, rows, N)
     out = torch.empty(shape, dtype=out_dtype, device=dev)
@@ -125,7 +140,12 @@ class MoELayer:
     """Device weights of one MoE layer and the C descriptor pointing at them."""
 
     def __init__(self, gate_w, w1: QuantProjection, w3: QuantProjection, w2: QuantProjection,
-                 top_k, norm_topk, act_dtype, n_shared=0, logit_bias=None):
+                 top_k, norm_topk, act_dtype, n_shared=0, logit_bias=None, one_token_act_softmax=False):
+        """one_token_act_softmax: forward(..., one_token=True) of a single
+        token routes on softmax probabilities rounded to act_dtype and
+        renormalises in act_dtype, as Mixtral's forward_one_token does
+        (gemq/inference/moe_block.py:280-283); every other call ranks the
+        logits with fp32 softmax weights."""
         E_total = w1.E
         self.n_shared = n_shared
         self.n_experts = E_total - n_shared
@@ -145,6 +165,11 @@ class MoELayer:
             norm_topk=int(self.norm_topk), gate_w=self.gate_w.data_ptr(),
             w1=w1.struct(), w3=w3.struct(), w2=w2.struct(),
             logit_bias=None if self.logit_bias is None else self.logit_bias.data_ptr())
+        self.one_token_act_softmax = bool(one_token_act_softmax)
+        self.desc_one_token = self.desc
+        if self.one_token_act_softmax:
+            self.desc_one_token = L.MoeqMoe.from_buffer_copy(self.desc)
+            self.desc_one_token.one_token_act_softmax = 1
         self._ws = None
 
     def workspace_size(self, T):
@@ -170,11 +195,15 @@ class MoELayer:
             self._ws = torch.empty(need, dtype=torch.uint8, device=device)
         return self._ws
 
-    def forward(self, x, out_dtype=None, want_logits=True, out=None, logits=None, gate_up_events=None):
+    def forward(self, x, out_dtype=None, want_logits=True, out=None, logits=None, gate_up_events=None,
+                one_token=False):
         """x [T, H] -> (out [T, H], logits [T, E] or None).  gate_up_events:
         optional pair of recorded torch.cuda.Event, re-recorded on the
-        current stream just before and after the gate/up launch."""
+        current stream just before and after the gate/up launch.  one_token:
+        the call is a forward_one_token (selects the one-token routing of
+        one_token_act_softmax layers)."""
         assert x.dim() == 2 and x.shape[1] == self.hidden, x.shape
+        desc = self.desc_one_token if one_token else self.desc
         if x.dtype != self.act_dtype:
             raise TypeError(f"activations are {x.dtype}, layer expects {self.act_dtype}")
         x = x.contiguous()
@@ -191,45 +220,71 @@ class MoELayer:
             e0, e1 = (e._as_parameter_ for e in gate_up_events)
             if not e0.value or not e1.value:
                 raise ValueError("gate_up_events must have been recorded once (torch creates them lazily)")
-            L.check(L.lib().moeq_moe_forward_timed(self.desc, L.ptr(x), T, L.ptr(out), L.dtype_code(odt),
+            L.check(L.lib().moeq_moe_forward_timed(desc, L.ptr(x), T, L.ptr(out), L.dtype_code(odt),
                                                    L.ptr(logits) if want_logits else None, L.ptr(ws),
                                                    ws.numel(), L.stream_handle(dev), e0, e1),
                     "moeq_moe_forward_timed")
             return out, (logits if want_logits else None)
-        L.check(L.lib().moeq_moe_forward(self.desc, L.ptr(x), T, L.ptr(out), L.dtype_code(odt),
+        L.check(L.lib().moeq_moe_forward(desc, L.ptr(x), T, L.ptr(out), L.dtype_code(odt),
                                          L.ptr(logits) if want_logits else None, L.ptr(ws), ws.numel(),
                                          L.stream_handle(dev)), "moeq_moe_forward")
         return out, (logits if want_logits else None)
 
 
 # ------------------------------------------- reference kernel-level surface
+# Build-layout projections derived from reference-stacked tensors, keyed on
+# the identity of those tensors.  An entry holds weak references to them and
+# their version counters: it is used only while every tensor is the same live,
+# unmodified object (a new tensor can reuse a freed address or a dead
+# object's id, but never a live weak reference), and is dropped as soon as
+# one of them is freed.  Nothing here keeps the source tensors alive: the
+# projection holds its own copies.
 _REPACK_CACHE = {}
 
 
-def _proj_from_stacked(wq, scales, zeros, nbits, wq_strides, zs_strides, K, group_size):
-    """Build-layout view of reference-stacked tensors (cached per storage)."""
-    key = (wq.data_ptr(), wq._version, scales.data_ptr(), scales._version, zeros.data_ptr(), zeros._version,
-           K, group_size, tuple(wq.shape))
+def _cached_proj(tensors, extra, build):
+    key = tuple(id(t) for t in tensors) + tuple(extra)
+    versions = tuple(t._version for t in tensors)
     hit = _REPACK_CACHE.get(key)
     if hit is not None:
-        return hit
-    nb = [int(b) for b in nbits.tolist()]
-    wst = [int(s) for s in wq_strides.tolist()]
-    zst = [int(s) for s in zs_strides.tolist()]
-    N = wq.shape[1]
-    G = K // group_size
-    flat_w, flat_s, flat_z = wq.reshape(-1), scales.reshape(-1), zeros.reshape(-1)
-    words, sc, ze = [], [], []
-    for e, b in enumerate(nb):
-        rows = -(-K // (32 // b))
-        words.append(flat_w[wst[e]:wst[e] + rows * N].view(rows, N))
-        sc.append(flat_s[zst[e]:zst[e] + G * N].view(G, N))
-        ze.append(flat_z[zst[e]:zst[e] + G * N].view(G, N))
-    proj = QuantProjection(words, sc, ze, nb, K, N, group_size, L.DQ_AFFINE)
-    if len(_REPACK_CACHE) > 64:
-        _REPACK_CACHE.clear()
-    _REPACK_CACHE[key] = proj
+        refs, vers, proj = hit
+        if vers == versions and all(r() is t for r, t in zip(refs, tensors)):
+            return proj
+    proj = build()
+
+    def drop(_ref, key=key):
+        _REPACK_CACHE.pop(key, None)
+
+    _REPACK_CACHE[key] = (tuple(weakref.ref(t, drop) for t in tensors), versions, proj)
     return proj
+
+
+def _proj_from_stacked(wq, scales, zeros, nbits, wq_strides, zs_strides, K, group_size):
+    """Build-layout view of reference-stacked tensors (GemLite zeros).  nbits,
+    wq_strides and group_size may be tensors or Python ints; zs_strides None
+    means the uniform scale offsets e * (K / g) * N the decode kernels assume
+    (fused_dequant_bmm.py:62, :218).  Host reads of the meta tensors happen
+    only when the projection is built, not per call."""
+    src = [t for t in (wq, scales, zeros, nbits, wq_strides, zs_strides, group_size) if torch.is_tensor(t)]
+    extra = (K,) + tuple(None if torch.is_tensor(t) else t for t in (nbits, wq_strides, zs_strides, group_size))
+
+    def build():
+        nb = [int(b) for b in nbits.tolist()] if torch.is_tensor(nbits) else [int(nbits)]
+        gs = int(group_size.reshape(-1)[0].item()) if torch.is_tensor(group_size) else int(group_size)
+        N = wq.shape[1]
+        G = K // gs
+        wst = [int(v) for v in wq_strides.tolist()] if torch.is_tensor(wq_strides) else [int(wq_strides)]
+        zst = [int(v) for v in zs_strides.tolist()] if zs_strides is not None else [e * G * N for e in range(len(nb))]
+        flat_w, flat_s, flat_z = wq.reshape(-1), scales.reshape(-1), zeros.reshape(-1)
+        words, sc, ze = [], [], []
+        for e, b in enumerate(nb):
+            rows = -(-K // (32 // b))
+            words.append(flat_w[wst[e]:wst[e] + rows * N].view(rows, N))
+            sc.append(flat_s[zst[e]:zst[e] + G * N].view(G, N))
+            ze.append(flat_z[zst[e]:zst[e] + G * N].view(G, N))
+        return QuantProjection(words, sc, ze, nb, K, N, gs, L.DQ_AFFINE)
+
+    return _cached_proj(src, extra, build)
 
 
 def _bm_for(m):
@@ -251,6 +306,17 @@ def _slot_tiles(expert_ids, rows_per_slot, bm):
     return tiles.contiguous(), n, A * nmt
 
 
+def silu_mul(x1, x3):
+    """fp16(silu(x1) * x3) computed in fp32 (moeq_silu_mul), the prologue of
+    fused_dequant_down_proj_triton (fused_dequant_bmm.py:236-239)."""
+    assert x1.shape == x3.shape and x1.dtype == x3.dtype == torch.float16
+    x1, x3 = x1.contiguous(), x3.contiguous()
+    out = torch.empty_like(x1)
+    L.check(L.lib().moeq_silu_mul(L.ptr(x1), L.ptr(x3), x1.numel(), L.ptr(out), L.stream_handle(x1.device)),
+            "moeq_silu_mul")
+    return out
+
+
 def dequant_group_gemm(x, indices, wq, scales, zeros, nbits, group_sizes, wq_strides, zs_strides,
                        compute_dtype=torch.float16):
     """out[a] = x @ dequantize(wq[indices[a]]), [A, M, N] fp16.
@@ -260,8 +326,7 @@ def dequant_group_gemm(x, indices, wq, scales, zeros, nbits, group_sizes, wq_str
     M, K = x.shape
     N = wq.shape[1]
     A = indices.shape[0]
-    gs = int(group_sizes[0].item()) if torch.is_tensor(group_sizes) else int(group_sizes)
-    proj = _proj_from_stacked(wq, scales, zeros, nbits, wq_strides, zs_strides, K, gs)
+    proj = _proj_from_stacked(wq, scales, zeros, nbits, wq_strides, zs_strides, K, group_sizes)
     bm = _bm_for(M)
     tiles, n, mt = _slot_tiles(indices.reshape(-1), M, bm)
     row_src = torch.arange(A * M, device=x.device, dtype=torch.int32) % M
@@ -277,10 +342,8 @@ def fused_dequant_up_proj(x, idx, w1, w3, w1_scales, w1_zeros, w3_scales, w3_zer
     _, K = x.shape
     N = w1.shape[1]
     A = idx.shape[0]
-    E = nbits.shape[0]
-    zst = torch.arange(E, device=x.device, dtype=torch.int32) * (K // group_size) * N
-    p1 = _proj_from_stacked(w1, w1_scales, w1_zeros, nbits, w_strides, zst, K, group_size)
-    p3 = _proj_from_stacked(w3, w3_scales, w3_zeros, nbits, w_strides, zst, K, group_size)
+    p1 = _proj_from_stacked(w1, w1_scales, w1_zeros, nbits, w_strides, None, K, group_size)
+    p3 = _proj_from_stacked(w3, w3_scales, w3_zeros, nbits, w_strides, None, K, group_size)
     tiles, n, mt = _slot_tiles(idx.reshape(-1), 1, 16)
     row_src = torch.zeros(A, dtype=torch.int32, device=x.device)
     xc = x.contiguous()
@@ -291,15 +354,14 @@ def fused_dequant_up_proj(x, idx, w1, w3, w1_scales, w1_zeros, w3_scales, w3_zer
 
 def fused_dequant_down_proj(x1, x3, idx, w2, w2_scales, w2_zeros, nbits, w_strides, group_size):
     """x2[a] = (silu(x1[a]) * x3[a]) @ deq(w2[idx[a]]) as [1, A*N] fp16.
-    gemq/triton_kernels/fused_dequant_bmm.py:264-312 (fp32 SiLU prologue,
-    :236-239; here the product is rounded to fp16 before the MFMA)."""
+    gemq/triton_kernels/fused_dequant_bmm.py:264-312.  The fp32 SiLU*mul
+    prologue (:236-239) runs as moeq_silu_mul, whose fp16 product the
+    grouped GEMM reads."""
     A = idx.shape[0]
     K = x1.shape[1] // A
     N = w2.shape[1]
-    E = nbits.shape[0]
-    h = (F.silu(x1.float()) * x3.float()).half().view(A, K)
-    zst = torch.arange(E, device=x1.device, dtype=torch.int32) * (K // group_size) * N
-    p2 = _proj_from_stacked(w2, w2_scales, w2_zeros, nbits, w_strides, zst, K, group_size)
+    h = silu_mul(x1, x3).view(A, K)
+    p2 = _proj_from_stacked(w2, w2_scales, w2_zeros, nbits, w_strides, None, K, group_size)
     tiles, n, mt = _slot_tiles(idx.reshape(-1), 1, 16)
     out = grouped_gemm(h, A, N, tiles, n, mt, 16, p2)
     return out.view(1, A * N)
@@ -308,11 +370,9 @@ def fused_dequant_down_proj(x1, x3, idx, w2, w2_scales, w2_zeros, nbits, w_strid
 def dequant_gemm(x, w_q, scales, zeros, nbits, group_size):
     """x @ dequantize(w_q), [M, N] fp16.  gemq/triton_kernels/dequant_gemm.py:150-193."""
     M, K = x.shape
-    dev = x.device
-    one = torch.zeros(1, dtype=torch.int32, device=dev)
-    nb = torch.tensor([int(nbits)], dtype=torch.int32, device=dev)
-    proj = _proj_from_stacked(w_q, scales, zeros, nb, one, one, K, int(group_size))
+    proj = _proj_from_stacked(w_q, scales, zeros, int(nbits), 0, None, K, int(group_size))
     bm = _bm_for(M)
+    one = torch.zeros(1, dtype=torch.int32, device=x.device)
     tiles, n, mt = _slot_tiles(one, M, bm)
     return grouped_gemm(x.contiguous(), M, w_q.shape[1], tiles, n, mt, bm, proj)
 
@@ -337,6 +397,6 @@ def pack_weights_over_cols(W_q, W_nbits, packing_bitwidth=32, transpose=True):
 
 __all__ = [
     "route", "route_from_logits", "permute", "grouped_gemm", "combine", "MoELayer",
-    "dequant_group_gemm", "fused_dequant_up_proj", "fused_dequant_down_proj", "dequant_gemm",
+    "silu_mul", "dequant_group_gemm", "fused_dequant_up_proj", "fused_dequant_down_proj", "dequant_gemm",
     "dequant_splitk_gemv", "pack_weights_over_cols", "unpack_words",
 ]

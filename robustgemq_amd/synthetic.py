@@ -37,9 +37,10 @@ class LayerConfig:
 
 
 CONFIGS = {
-    # OLMoE-1B-7B shaped, uniform 2-bit, T = 128
+    # OLMoE-1B-7B shaped, uniform 2-bit, T = 128; and T = 2048, the
+    # size BASELINE.json's north-star target quotes this layer at
     "olmoe_2bit": LayerConfig("olmoe_2bit", "olmoe", 2048, 1024, 64, 8, False, 64, ("fixed", 2),
-                              torch.float16, runs={"prefill": (128,)}),
+                              torch.float16, runs={"prefill": (128, 2048)}),
     # mixed 2/3/4 bits 50/25/25
     "olmoe_mixed": LayerConfig("olmoe_mixed", "olmoe", 2048, 1024, 64, 8, False, 64,
                                ("mix", {2: 32, 3: 16, 4: 16}), torch.float16,
@@ -158,7 +159,8 @@ def build_block(cfg: LayerConfig, weights, device="cuda"):
         layer = block._layer
         from .ops import MoELayer
         block._layer = MoELayer(layer.gate_w, layer.w1, layer.w3, layer.w2, layer.top_k, layer.norm_topk,
-                                layer.act_dtype, n_shared=layer.n_shared, logit_bias=weights["bias"].to(device))
+                                layer.act_dtype, n_shared=layer.n_shared, logit_bias=weights["bias"].to(device),
+                                one_token_act_softmax=layer.one_token_act_softmax)
     return block.to(device)
 
 

@@ -144,21 +144,28 @@ def test_one_token_forward_routing(device, name):
     x = make_x(cfg, 1, seed=11)
     ref, ref_lg, ref_idx, ref_w = _oracle(cfg, w, dense, x)
     layer = block._layer
+    k, E, ns = layer.top_k, layer.n_experts, layer.n_shared
+    if layer.one_token_act_softmax:  # Mixtral's forward_one_token router (moe_block.py:280-283)
+        ref_idx, ref_w, _, fragile = orr.topk_route_act_softmax(ref_lg, k, "bf16")
+        assert not fragile.any()
+        ref = om.moe_from_routing(x.float().numpy(), ref_idx, ref_w, *dense[:3], dense[3])
     xd = x.to("cuda")
-    out32, lg = layer.forward(xd, out_dtype=torch.float32, want_logits=True)
+    out32, lg = layer.forward(xd, out_dtype=torch.float32, want_logits=True, one_token=True)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(lg.float().cpu().numpy().view(np.uint32), ref_lg.view(np.uint32))
-    k, E, ns = layer.top_k, layer.n_experts, layer.n_shared
     offs, ws = layer.workspace_layout(1), layer._ws
 
     def arr(i, n, dt=torch.int32):
         return ws[offs[i]:offs[i] + 4 * n].view(dt).cpu().numpy()
 
     np.testing.assert_array_equal(arr(0, k), ref_idx.reshape(-1))
-    _, _, w2 = ops.route(xd, layer.gate_w, k, layer.norm_topk, logit_bias=layer.logit_bias)
     wt = arr(1, k, torch.float32)
-    np.testing.assert_array_equal(wt.view(np.uint32), to_np(w2).reshape(-1).view(np.uint32))
-    np.testing.assert_allclose(wt, ref_w.reshape(-1), rtol=2e-6, atol=1e-7)
+    if layer.one_token_act_softmax:
+        np.testing.assert_array_equal(wt.view(np.uint32), ref_w.reshape(-1).view(np.uint32))
+    else:
+        _, _, w2 = ops.route(xd, layer.gate_w, k, layer.norm_topk, logit_bias=layer.logit_bias)
+        np.testing.assert_array_equal(wt.view(np.uint32), to_np(w2).reshape(-1).view(np.uint32))
+        np.testing.assert_allclose(wt, ref_w.reshape(-1), rtol=2e-6, atol=1e-7)
     ref_perm = orr.permute(ref_idx, E, ns)
     rows = k + ns
     for i, key, n in ((2, "counts", E + ns), (3, "offsets", E + ns + 1), (4, "row_token", rows),
@@ -172,6 +179,50 @@ def test_one_token_forward_routing(device, name):
     np.testing.assert_array_equal(tiles, want)
     got = to_np(out32)
     assert relative_error(got, ref) <= REL_L2 and float(np.abs(got - ref).max()) <= MAX_ABS
+
+
+def test_mixtral_one_token_routing_ties(device):
+    """Mixtral's forward_one_token ranks bf16 softmax probabilities and
+    renormalises in bf16 (moe_block.py:280-283).  1024 single-token forwards:
+    the selection and weights the forward leaves in its workspace equal the
+    oracle's restatement bit for bit (tokens whose fp32 softmax sits on a bf16
+    rounding midpoint aside, where any fp32 softmax may round either way);
+    the tokens whose 2nd and 3rd probabilities tie in bf16 are counted, and
+    torch's own softmax/topk on the device is compared as a second reading
+    (its tie order is unspecified, so it may differ only at ties)."""
+    import torch.nn.functional as F
+    cfg, w, block, dense = _layer("mixtral_small")
+    layer = block._layer
+    T, k = 1024, layer.top_k
+    x = make_x(cfg, T, seed=13)
+    gate = w["gate"].to(torch.bfloat16).float().numpy()
+    ref_lg = orr.router_logits(x.float().numpy(), gate, "bf16")
+    ref_idx, ref_w, p, fragile = orr.topk_route_act_softmax(ref_lg, k, "bf16")
+    offs = layer.workspace_layout(1)
+    xd = x.to("cuda")
+    gi, gw = [], []
+    for t in range(T):
+        layer.forward(xd[t:t + 1], want_logits=False, one_token=True)
+        ws = layer._ws
+        gi.append(ws[offs[0]:offs[0] + 4 * k].view(torch.int32).clone())
+        gw.append(ws[offs[1]:offs[1] + 4 * k].view(torch.float32).clone())
+    got_idx = torch.stack(gi).cpu().numpy()
+    got_w = torch.stack(gw).cpu().numpy()
+    keep = ~fragile
+    np.testing.assert_array_equal(got_idx[keep], ref_idx[keep])
+    np.testing.assert_array_equal(got_w[keep].view(np.uint32), ref_w[keep].view(np.uint32))
+    srt = -np.sort(-p, axis=1)
+    tie = srt[:, k - 1] == srt[:, k]
+    lg_rank = orr.topk_route(ref_lg, k, True)[0]
+    changed = (np.sort(lg_rank, 1) != np.sort(ref_idx, 1)).any(1)
+    tp = F.softmax(torch.from_numpy(ref_lg).to("cuda", torch.bfloat16), dim=-1)
+    tw, ti = torch.topk(tp, k, dim=-1)
+    agree = (np.sort(ti.cpu().numpy(), 1) == np.sort(got_idx, 1)).all(1)
+    _say(f"    {T} tokens: {int(tie.sum())} bf16 ties at the top-{k} boundary, {int(changed.sum())} selections "
+         f"differ from logit ranking, {int(fragile.sum())} near-midpoint tokens; torch.topk on the device "
+         f"differs on {int((~agree).sum())} ({int((~agree & tie).sum())} of them at ties)")
+    assert not (~agree & ~tie & ~fragile).any()
+    assert not (changed & ~tie).any()  # logit ranking and probability ranking part only at ties
 
 
 def test_forward_timed_matches_forward(device):
@@ -245,6 +296,51 @@ def test_decode_equals_prefill_and_is_deterministic(device):
     assert torch.equal(a, b) and not torch.isnan(a).any()
 
 
+@pytest.mark.parametrize("T", [128, 512, 2048])
+def test_prefill_classes_write_every_output(device, T):
+    """The 48-, 96- and 160-row tile classes (OLMoE T = 128 / 512 / 2048,
+    with partial last tiles and the mixed block-count schedule) write every
+    row of h and y they later read: a workspace filled with NaN gives the
+    same output, bit for bit, as one filled with zeros, and no NaN."""
+    _say(f"[layer] poisoned workspace, olmoe_mixed T={T}")
+    cfg, w, block, dense = _layer("olmoe_mixed")
+    layer = block._layer
+    x = make_x(cfg, T, seed=31).to("cuda")
+    need = layer.workspace_size(T)
+    outs = []
+    for fill in (0.0, float("nan")):
+        layer._ws = torch.full((need // 2 + 1,), fill, dtype=torch.float16, device="cuda").view(torch.uint8)
+        outs.append(layer.forward(x, out_dtype=torch.float32, want_logits=False)[0].clone())
+    layer._ws = None
+    _say(f"    plan {layer.plan(T)}")
+    assert not torch.isnan(outs[1]).any()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_bf16_activations_beyond_fp16_range(device):
+    """bf16 layers feed the expert GEMMs fp16 activations and keep the
+    intermediate products in fp16, as the reference's kernels emit fp16
+    (dequant_group_gemm.py:138, :181; fused_dequant_bmm.py:152-153, :292).
+    A token with an activation beyond 65504 therefore has a non-finite output
+    row (the overflow shows; it is never a finite wrong value); its routing
+    is still exact and every other token is unaffected and within the bar."""
+    _say("[layer] bf16 activations beyond the fp16 range")
+    cfg, w, block, dense = _layer("qwen3_mixed")
+    layer = block._layer
+    T, bad = 64, 5
+    x = make_x(cfg, T, seed=9)
+    x[bad, 7] = 1.0e5
+    ref, ref_lg, ref_idx, ref_w = _oracle(cfg, w, dense, x)
+    xd = x.to("cuda")
+    out32, lg = layer.forward(xd, out_dtype=torch.float32, want_logits=True)
+    np.testing.assert_array_equal(lg.float().cpu().numpy().view(np.uint32), ref_lg.view(np.uint32))
+    got = to_np(out32)
+    assert not np.isfinite(got[bad]).all()
+    ok = np.arange(T) != bad
+    assert np.isfinite(got[ok]).all()
+    assert relative_error(got[ok], ref[ok]) <= REL_L2 and float(np.abs(got[ok] - ref[ok]).max()) <= MAX_ABS
+
+
 def test_block_api_conventions(device):
     _say("[layer] API conventions")
     cfg, w, block, dense = _layer("ref_test")
@@ -300,10 +396,41 @@ def test_reference_kernel_surface(device):
     for a, e in enumerate([3, 0, 2]):
         ref = x[:1].float().numpy() @ dense[e]
         assert relative_error(to_np(x1[0, a * N:(a + 1) * N]).astype(np.float32), ref[0]) < 1e-3
+    # fused_dequant_down_proj: fp32 SiLU*mul of the up projection's outputs,
+    # rounded to fp16 (fused_dequant_bmm.py:236-239), then the down GEMV
+    x1s = torch.from_numpy((rng.standard_normal((1, 3 * K)) * 2).astype(np.float16))
+    x3s = torch.from_numpy((rng.standard_normal((1, 3 * K)) * 2).astype(np.float16))
+    x2 = ops.fused_dequant_down_proj(x1s.cuda(), x3s.cuda(), ind, wq, scales, zeros, nb, wst, g)
+    assert x2.shape == (1, 3 * N) and x2.dtype == torch.float16
+    a1, a3 = x1s.float().numpy()[0], x3s.float().numpy()[0]
+    h = (a1 / (1.0 + np.exp(-a1)) * a3).astype(np.float16).astype(np.float32)
+    for a, e in enumerate([3, 0, 2]):
+        ref = h[a * K:(a + 1) * K] @ dense[e]
+        assert relative_error(to_np(x2[0, a * N:(a + 1) * N]).astype(np.float32), ref) < 1e-3
     y = ops.dequant_gemm(x.cuda(), words[1].cuda(), sc[1].cuda(), ze[1].cuda(), 2, g)
     assert relative_error(to_np(y).astype(np.float32), x.float().numpy() @ dense[1]) < 1e-3
     v = ops.dequant_splitk_gemv(x[:1].cuda(), words[2].cuda(), sc[2].cuda(), ze[2].cuda(), 3, g)
     assert relative_error(to_np(v).astype(np.float32), x[:1].float().numpy() @ dense[2]) < 1e-3
+    # the repacked-weight cache follows the tensors, not their addresses: new
+    # weights of the same shape (the caching allocator hands back the freed
+    # block) and an in-place change both take effect
+    xd = x.cuda()
+    for trial in range(3):
+        codes = rng.integers(0, 4, size=(N, K)).astype(np.uint8)
+        wt = torch.from_numpy(oq.pack_cols(codes, 2)).cuda()
+        st, zt = sc[1].cuda(), ze[1].cuda()
+        gi = np.arange(K) // g
+        dn = oq.dequant_affine(codes.T.astype(np.float16), sc[1].numpy()[gi], ze[1].numpy()[gi]).astype(np.float32)
+        yt = ops.dequant_gemm(xd, wt, st, zt, 2, g)
+        assert relative_error(to_np(yt).astype(np.float32), x.float().numpy() @ dn) < 1e-3, trial
+        del wt, st, zt, yt
+    st, zt = sc[1].cuda(), ze[1].cuda()
+    wt = words[1].cuda()
+    before = ops.dequant_gemm(xd, wt, st, zt, 2, g).clone()
+    st.mul_(2)  # in place: the version counter moves
+    after = ops.dequant_gemm(xd, wt, st, zt, 2, g)
+    fresh = ops.dequant_gemm(xd, wt.clone(), st.clone(), zt.clone(), 2, g)  # new tensors: built anew
+    assert torch.equal(after, fresh) and not torch.equal(after, before)
 
 
 # ------------------------------------------------------------- from_hf

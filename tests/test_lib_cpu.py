@@ -118,6 +118,38 @@ def test_grouped_gemm_argument_checks():
     assert rc == -1 and "bm" in msg
 
 
+def test_silu_mul_argument_checks():
+    lib = L.lib()
+    f = ctypes.c_void_p(0x1000)
+    rc, msg = _err(lib.moeq_silu_mul(f, f, 12, f, None))
+    assert rc == -1 and "multiple of 8" in msg
+    rc, msg = _err(lib.moeq_silu_mul(None, f, 16, f, None))
+    assert rc == -1 and "null" in msg
+
+
+def test_activation_rows_2gib_guard():
+    """Row tiles of 32+ rows address activation rows with 32-bit offsets: the
+    operator refuses activations whose rows end past 2 GiB (16-row tiles use
+    64-bit addresses and take any), and QuantLinear slices its rows so every
+    slice fits."""
+    from types import SimpleNamespace
+
+    from robustgemq_amd import ops
+
+    def fake(rows, stride, esize=2):
+        return SimpleNamespace(shape=(rows, stride), stride=lambda i: stride, element_size=lambda: esize)
+
+    K = 4096
+    fit = (1 << 31) // (K * 2)
+    assert ops.a_rows_addressable(fake(fit, K), 128)
+    assert not ops.a_rows_addressable(fake(fit + 1, K), 128)
+    assert not ops.a_rows_addressable(fake(fit + 1, K), 32)
+    assert ops.a_rows_addressable(fake(4 * fit, K), 16)
+    for K in (128, 2048, 4096, 14336, 1 << 20):
+        rows_max = max(16, (ops.A_ROWS_MAX_BYTES // (K * 2)) // 16 * 16)  # QuantLinear's slice
+        assert ops.a_rows_addressable(fake(rows_max, K), 128) or rows_max == 16
+
+
 def test_max_tiles_bounds_every_routing():
     """The host bound on row tiles must cover any routing the device can see."""
     lib = L.lib()

@@ -236,6 +236,48 @@ def test_topk_brute_force_and_softmax():
     np.testing.assert_allclose(wn.sum(axis=1), 1.0, rtol=1e-6)
 
 
+@pytest.mark.parametrize("dtype,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16)])
+def test_act_softmax_router_matches_torch_ops(dtype, tdt):
+    """topk_route_act_softmax against torch's own CPU ops running the lines of
+    Mixtral's forward_one_token (moe_block.py:281-283) on 16-bit scores.
+    Probabilities and weights must agree bit for bit, and the selection
+    wherever the k-th and (k+1)-th rounded probabilities differ (torch's tie
+    order is unspecified).  Ranking logits instead of rounded probabilities,
+    renormalising in fp32 or skipping the rounding of the sum each fail this:
+    with 8 experts about one token in a hundred has a tie at the top-2
+    boundary, and the sum's rounding changes most weights."""
+    import torch.nn.functional as F
+    rng = np.random.default_rng(11)
+    T, E, k = 20000, 8, 2
+    lg = route.round_to(rng.normal(0, 0.7, size=(T, E)).astype(np.float32), dtype)
+    idx, w, p, fragile = route.topk_route_act_softmax(lg, k, dtype)
+    scores = torch.from_numpy(lg).to(tdt)
+    tp = F.softmax(scores, dim=-1)
+    tw, ti = torch.topk(tp, k, dim=-1)
+    tw /= tw.sum(dim=-1, keepdim=True)
+    # probabilities differ only where an fp32 value sits on a rounding midpoint
+    differ = (p != tp.float().numpy()).any(1)
+    assert not (differ & ~fragile).any() and fragile.mean() < 2e-2, (differ.sum(), fragile.sum())
+    keep = ~fragile
+    idx, w, p, lg, tw, ti = idx[keep], w[keep], p[keep], lg[keep], tw[keep], ti[keep]
+    srt = -np.sort(-p, axis=1)
+    untied = srt[:, k - 1] != srt[:, k]
+    ties = int((~untied).sum())
+    assert (50 if dtype == "bf16" else 10) < ties < 1000, ties  # the sample does exercise the tie rule
+    np.testing.assert_array_equal(np.sort(idx[untied], 1), np.sort(ti.numpy()[untied], 1))
+    distinct = untied & (np.diff(srt[:, :k + 1], axis=1) != 0).all(1)  # no tie inside the top k either
+    np.testing.assert_array_equal(idx[distinct], ti.numpy()[distinct])
+    # where tied, both selections hold the same values, so the weights agree
+    np.testing.assert_array_equal(w.view(np.uint32), tw.float().numpy().view(np.uint32))
+    order = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    np.testing.assert_array_equal(idx, order)  # equal values: lower index first
+    # the rounded sum differs from the fp32 one often enough to matter
+    w32 = np.take_along_axis(p, idx.astype(np.int64), 1)
+    w32 = route.round_to((w32 / w32.sum(1, keepdims=True)).astype(np.float32), dtype)
+    assert (w32 != w).any()
+    assert np.array_equal(idx, route.topk_route(lg, k, True)[0]) is False
+
+
 def test_permute_matches_reference_loop():
     rng = np.random.default_rng(4)
     for T, k, E in ((1, 1, 1), (1, 8, 64), (37, 2, 8), (256, 8, 64), (300, 6, 64)):
