@@ -9,7 +9,8 @@
  *     memory is a caller-provided workspace whose size the *_workspace_size()
  *     query returns, so the calls can be captured into a HIP graph,
  *   - is reentrant across streams (no hidden global state besides the
- *     thread-local error string).
+ *     thread-local error string), except moeq_moe_forward_static, whose
+ *     static per-GPU scratch array makes overlapping calls on one GPU race.
  *
  * Citations are path:line into lcj1111/RobustGEMQ and name the reference
  * interface each entry point replaces.
@@ -243,6 +244,24 @@ size_t moeq_moe_workspace_size(const moeq_moe *m, int64_t T);
 int moeq_moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out,
                      int out_dtype, void *logits_out, void *ws,
                      size_t ws_bytes, void *stream);
+
+/* Size of the static scratch array moeq_moe_forward_static uses on each GPU
+ * (64 MiB: moeq_moe_workspace_size of up to about 1024 tokens of the
+ * OLMoE / Qwen3 / DeepSeek-shaped layers, 800 of the Mixtral-shaped one). */
+#define MOEQ_STATIC_SCRATCH_BYTES (64u << 20)
+
+/* moeq_moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Scratch memory is a file-scope device array of MOEQ_STATIC_SCRATCH_BYTES per
+ * GPU, which the library holds until the process ends; the call allocates
+ * nothing and returns MOEQ_ERR_WORKSPACE, launching nothing, when
+ * moeq_moe_workspace_size(m, T) exceeds the array.  It runs on the current
+ * device, which must be the stream's.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams or threads) race
+ * and must be serialised by the caller.  Same results as moeq_moe_forward. */
+int moeq_moe_forward_static(const moeq_moe *m, const void *x, int64_t T, void *out,
+                            int out_dtype, void *logits_out, void *stream);
 
 /* ------------------------------------------------------------ introspection
  * No reference counterpart: launch-plan queries used by the Python host

@@ -103,6 +103,8 @@ SIGNATURES = {
     "moeq_moe_workspace_size": (c_size_t, [ctypes.POINTER(MoeqMoe), c_int64]),
     "moeq_moe_forward": (c_int, [ctypes.POINTER(MoeqMoe), c_void_p, c_int64, c_void_p, c_int,
                                  c_void_p, c_void_p, c_size_t, c_void_p]),
+    "moeq_moe_forward_static": (c_int, [ctypes.POINTER(MoeqMoe), c_void_p, c_int64, c_void_p, c_int,
+                                        c_void_p, c_void_p]),
     "moeq_gemm_tile_n": (c_int, [c_int, c_int]),
     "moeq_moe_plan": (c_int, [ctypes.POINTER(MoeqMoe), c_int64, c_void_p]),
     "moeq_moe_workspace_layout": (c_int, [ctypes.POINTER(MoeqMoe), c_int64, c_void_p]),
