@@ -35,11 +35,12 @@ __host__ __device__ constexpr int tile_rows(int bm) {
 
 // The grouped GEMM instantiates, per class, kernel variants for 16-row block
 // counts {1, 2} (bm 16), {2, 3} (32), {2, 4, 6} (64), {2, 4, 8, 10} (128) and
-// {2, 4, 8, 16} (256); a tile of b blocks runs the smallest count >= b.  The
-// schedule cuts experts into tiles of the largest count and of the one below
-// it, returned here.
+// {2, 4, 8, 10, 16} (256); a tile of b blocks runs the smallest count >= b.
+// The schedule cuts experts into tiles of the largest count and of the one
+// below it, returned here (for bm 256, 10: an expert of 17..20 blocks takes two
+// tiles of about half, not 16 blocks and a remainder).
 __host__ __device__ constexpr int tile_blocks_below(int bm) {
-  return bm == 16 ? 1 : bm == 32 ? 2 : bm == 64 ? 4 : bm == 128 ? 8 : bm == 256 ? 8 : 0;
+  return bm == 16 ? 1 : bm == 32 ? 2 : bm == 64 ? 4 : bm == 128 ? 8 : bm == 256 ? 10 : 0;
 }
 
 // ------------------------------------------------------- device helpers

@@ -456,19 +456,17 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
     if (mb_act <= 2) MOEQ_T(2); else MOEQ_T(3);
   } else if constexpr (BM == 64) {
     if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else MOEQ_T(6);
-  } else if constexpr (BM == 128) {
-    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else if (mb_act <= 8) MOEQ_T(8); else MOEQ_T(10);
   } else {
-    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else if (mb_act <= 8) MOEQ_T(8); else MOEQ_T(16);
+    static_assert(BM == 128, "the 256-row class has its own kernel (gemm_wide.h)");
+    if (mb_act <= 2) MOEQ_T(2); else if (mb_act <= 4) MOEQ_T(4); else if (mb_act <= 8) MOEQ_T(8); else MOEQ_T(10);
   }
 #undef MOEQ_T
 }
 
 // Two work-groups per CU for the 32..128 classes (tiles of up to 48..160
-// rows) and one 8-wave group for the 256-row shape (its two A buffers take
-// 128 KB of LDS): 2 waves per SIMD.
+// rows): 2 waves per SIMD.
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, bool KS, bool MB2 = true>
-__global__ __launch_bounds__(NW * 64, (BM == 16 || BM == 256) ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
   // The grid is sized for the host-side bound on row tiles; blocks past the
   // real count (read from the device schedule) exit together.  Work-groups
   // are dealt to the 8 XCDs round-robin, so the live ones are renumbered to
@@ -534,10 +532,10 @@ template <> struct Shape<64, true> { static constexpr int NW = 4, NB = 2; };
 template <> struct Shape<64, false> { static constexpr int NW = 4, NB = 4; };
 template <> struct Shape<128, true> { static constexpr int NW = 4, NB = 2; };
 template <> struct Shape<128, false> { static constexpr int NW = 4, NB = 4; };
-// 256-row tiles: 8 waves, each with all rows and 16 (gate + up) or 32 columns,
-// so one dequantized B fragment feeds 16 row blocks.
-template <> struct Shape<256, true> { static constexpr int NW = 8, NB = 1; };
-template <> struct Shape<256, false> { static constexpr int NW = 8, NB = 2; };
+// 256-row tiles (gemm_wide.h): 4 waves, one per SIMD, each with all rows and
+// 32 + 32 (gate + up) or 64 columns: 256 accumulators per wave in the AGPRs.
+template <> struct Shape<256, true> { static constexpr int NW = 4, NB = 2; };
+template <> struct Shape<256, false> { static constexpr int NW = 4, NB = 4; };
 
 // moeq_grouped_gemm for callers that know the most rows any tile holds
 // (max_rows > 0; the layer forward: at most T per expert), which lets 16-row

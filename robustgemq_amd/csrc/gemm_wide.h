@@ -1,0 +1,270 @@
+// 256-row prefill tile of the grouped GEMM: one wave per SIMD, accumulators
+// resident in AGPRs.  Included by gemm_bm256.hip.
+//
+// The prefill tiles of gemm_impl.h run two waves per SIMD, so each wave has
+// 256 registers; 160 of them hold accumulators and the dequantized B fragment
+// of one MFMA step feeds at most 10 row blocks.  Here a work-group of four
+// waves owns a CU (one wave per SIMD, 512 registers each): the 256
+// accumulators of a wave (16 row blocks x 4 fragments of 16 columns) live in
+// the AGPRs and the VGPRs hold the operands, so
+//   * one dequantized B fragment feeds 16 row blocks (16 MFMAs per 14 or so
+//     VALU instructions of unpacking instead of 10), and
+//   * the fragments of step t + 1 are unpacked while step t's MFMAs run (two
+//     register sets), with no register pressure pushing the unpacking back
+//     into the MFMA stream.
+// The MFMAs are written as inline asm with "+a" accumulator operands, the one
+// way to keep the compiler from staging accumulators through VGPRs (with the
+// builtin it parks them in AGPRs as spill slots and copies them back and
+// forth).  The compiler therefore does not see them as MFMAs, and the hazards
+// it would otherwise resolve are handled here:
+//   * a VALU write of a VGPR followed by an MFMA reading it needs two wait
+//     states: every MFMA is preceded by s_nop 1 (the B fragments are VALU
+//     results; the accumulators' zero initialisation is a VALU write too);
+//   * an MFMA's result read by a VALU instruction (the epilogue's AGPR reads)
+//     needs the MFMA's passes plus a few wait states: the k loop ends with 24
+//     wait states behind scheduling barriers;
+//   * consecutive MFMAs on one accumulator are at least 7 MFMAs apart (4
+//     fragments x 2 row blocks), far more than the dependent-accumulate
+//     latency.
+// A rows are staged global -> LDS exactly as in gemm_impl.h (XOR-swizzled
+// 16-byte units, two 64 KB buffers).
+#pragma once
+
+#include "gemm_impl.h"
+
+namespace moeq {
+
+__device__ __forceinline__ void mfma_agpr(f32x4 &acc, const f16x8 &a, const f16x8 &b) {
+  asm("s_nop 1\n\tv_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+template <int NB, int NP, int EPI, int ODT, int BITS, int DQ, int MBA>
+__device__ __forceinline__ void wide_tile(const GemmArgs &g, int e, int row0, int mcount, int nt, int c0, int c1,
+                                          uint4 (*As0)[16], uint4 (*As1)[16]) {
+  constexpr int NW = 4, NT = NW * 64;
+  static_assert(MBA <= 16, "a wave holds at most 16 row blocks");
+  static_assert(NP * NB * MBA * 4 <= 256, "accumulators exceed the AGPRs");
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, kb = lane >> 4;
+  const int N = g.N;
+  const int n_wave = nt * (NW * NB * 16) + wave * NB * 16;
+
+  const char *wbase[NP];
+  const char *sbase[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    wbase[p] = reinterpret_cast<const char *>(g.p[p].words + g.p[p].word_off[e]);
+    sbase[p] = reinterpret_cast<const char *>(g.p[p].sz + g.p[p].sz_off[e]);
+  }
+  uint32_t woff[NB], soff[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int ncol = min(n_wave + nb * 16 + l16, N - 1);
+    woff[nb] = uint32_t((ncol * 4 + kb) * BITS * 4);
+    soff[nb] = uint32_t(ncol * 4);
+  }
+  const int64_t chunk_bytes = int64_t(N) * 16 * BITS;
+  const uint32_t grp_bytes = uint32_t(N) * 4u;
+
+  f32x4 acc[NP][MBA][NB];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int mb = 0; mb < MBA; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[p][mb][nb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  auto load_b = [&](int c, uint32_t (&w)[NP][NB][BITS], uint32_t (&s)[NP][NB]) {
+    const int k = c * 128 + 32 * kb;
+    const uint32_t grp = uint32_t(g.gshift >= 0 ? k >> g.gshift : k / g.group_size);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const char *wc = wbase[p] + int64_t(c) * chunk_bytes;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        load_slice<BITS>(reinterpret_cast<const uint32_t *>(wc + woff[nb]), w[p][nb]);
+        s[p][nb] = *reinterpret_cast<const uint32_t *>(sbase[p] + (grp * grp_bytes + soff[nb]));
+      }
+    }
+  };
+
+  // A staging: MBA * 256 units of 16 bytes per chunk, MBA per thread.
+  constexpr int SEGS = MBA * 16 * 16 / NT;
+  const char *abytes = static_cast<const char *>(g.a);
+  uint32_t aoff[SEGS];
+#pragma unroll
+  for (int j = 0; j < SEGS; ++j) {
+    const int gu = (j * NW + wave) * 64 + lane;
+    const int r = gu >> 4, pu = gu & 15, u = pu ^ (r & 15);
+    const int rr = row0 + min(r, mcount - 1);
+    const int64_t src = g.row_src ? int64_t(g.row_src[rr]) : int64_t(rr);
+    aoff[j] = uint32_t((src * g.lda + u * 8) * 2);
+  }
+  const __amdgpu_buffer_rsrc_t arsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(abytes), (short)0, 0x7fffffff, 0x00020000);
+  auto load_a = [&](int c, uint4 (*dstA)[16]) {
+#pragma unroll
+    for (int j = 0; j < SEGS; ++j) {
+      char *dst = reinterpret_cast<char *>(&dstA[0][0]) + (j * NW + wave) * 64 * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_void *)dst, 16, aoff[j], uint32_t(c) * 256u, 0, 0);
+    }
+  };
+
+  uint32_t w0[NP][NB][BITS], w1[NP][NB][BITS], s0[NP][NB], s1[NP][NB];
+  f16x8 Bc[NP][NB];
+  // Each MFMA step runs as MBA regions, one per row block, fenced by
+  // scheduling barriers so the work stays spread out: the row block's NP * NB
+  // MFMAs, an even share of the next step's unpacking (NP * NB * 4 pairs per
+  // step), and the LDS read of the A fragment two row blocks ahead (into the
+  // next step while the chunk lasts; a chunk's first two are read after its
+  // barrier).
+  constexpr int PAIRS = NP * NB * 4;
+  auto chunk = [&](int c, uint4 (*Ard)[16], uint4 (*Awr)[16], const uint32_t (&wc)[NP][NB][BITS],
+                   const uint32_t (&sc)[NP][NB], uint32_t (&wn)[NP][NB][BITS], uint32_t (&sn)[NP][NB]) {
+    // next chunk fetched unconditionally (the last chunk re-reads itself)
+    const int cn = min(c + 1, c1 - 1);
+    load_a(cn, Awr);
+    load_b(cn, wn, sn);
+    auto read_a = [&](int t, int mb) {
+      return __builtin_bit_cast(f16x8, Ard[mb * 16 + l16][(4 * kb + t) ^ l16]);
+    };
+    f16x8 Aq[4 * MBA + 2];  // fragments in (step, row block) order
+    Aq[0] = read_a(0, 0);
+    if constexpr (MBA > 1) Aq[1] = read_a(0, 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f16x8 Bn[NP][NB];
+#pragma unroll
+      for (int mb = 0; mb < MBA; ++mb) {
+        const int q = t * MBA + mb + 2;  // fragment read two row blocks ahead
+        if (q < 4 * MBA) Aq[q] = read_a(q / MBA, q % MBA);
+#pragma unroll
+        for (int j = mb * PAIRS / MBA; j < (mb + 1) * PAIRS / MBA; ++j) {
+          const int f = j >> 2, d = j & 3, p = f / NB, nb = f % NB;
+          const f16x2 o = t < 3 ? deq_pair<BITS, DQ>(wc[p][nb], sc[p][nb], t + 1, d)
+                                : deq_pair<BITS, DQ>(wn[p][nb], sn[p][nb], 0, d);
+          Bn[p][nb][2 * d] = o[0];
+          Bn[p][nb][2 * d + 1] = o[1];
+        }
+        const f16x8 A = Aq[t * MBA + mb];
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) mfma_agpr(acc[p][mb][nb], A, Bc[p][nb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) Bc[p][nb] = Bn[p][nb];
+    }
+    __syncthreads();
+  };
+  if (c0 < c1) {
+    load_a(c0, As0);
+    load_b(c0, w0, s0);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) Bc[p][nb] = deq_frag<BITS, DQ>(w0[p][nb], s0[p][nb], 0);
+  // pairs of chunks, then an odd last one: no branch inside the loop body,
+  // whose join would have the accumulators copied out of the AGPRs and back
+  int c = c0;
+  for (; c + 1 < c1; c += 2) {
+    chunk(c, As0, As1, w0, s0, w1, s1);
+    chunk(c + 1, As1, As0, w1, s1, w0, s0);
+  }
+  if (c < c1) chunk(c, As0, As1, w0, s0, w1, s1);
+  // the last MFMAs' results are read by VALU instructions below
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+
+  // epilogue: D[row = 16 mb + 4 (lane / 16) + i][col = lane % 16], as gemm_tile's
+  constexpr int OES = (EPI == MOEQ_EPI_SILU_MUL || ODT != MOEQ_F32) ? 2 : 4;
+  const int64_t ldo_b = g.ldo * OES;
+  char *const tile_out =
+      static_cast<char *>(g.out) + (int64_t(blockIdx.z) * g.split_stride + int64_t(row0) * g.ldo) * OES;
+  const uint32_t lane_off = uint32_t(4 * kb) * uint32_t(ldo_b) + uint32_t((n_wave + l16) * OES);
+  auto put = [&](int mb, int nb, int i) {
+    char *p = tile_out + int64_t(16 * mb + i) * ldo_b + (lane_off + uint32_t(nb * 16 * OES));
+    if constexpr (EPI == MOEQ_EPI_SILU_MUL) {
+      *reinterpret_cast<uint16_t *>(p) = f32_to_f16_bits(silu_mul(acc[0][mb][nb][i], acc[NP - 1][mb][nb][i]));
+    } else if constexpr (ODT == MOEQ_F32) {
+      *reinterpret_cast<float *>(p) = acc[0][mb][nb][i];
+    } else {
+      *reinterpret_cast<uint16_t *>(p) = f32_to_f16_bits(acc[0][mb][nb][i]);
+    }
+  };
+#pragma unroll
+  for (int mb = 0; mb < MBA; ++mb) {
+    if (16 * (mb + 1) <= mcount) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (n_wave + nb * 16 >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) put(mb, nb, i);
+      }
+    } else if (16 * mb < mcount) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (n_wave + nb * 16 >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (16 * mb + 4 * kb + i < mcount) put(mb, nb, i);
+      }
+    }
+  }
+}
+
+// One work-group of four waves per CU; the LDS holds two 64 KB A buffers.
+template <int NB, int NP, int EPI, int ODT>
+__global__ __launch_bounds__(256, 1) void wide_gemm_kernel(GemmArgs g) {
+  const unsigned V = unsigned(*g.n_tiles) * unsigned(g.n_ntiles);
+  const unsigned b = blockIdx.x;
+  if (b >= V) return;
+  // XCD-aware renumbering, as grouped_gemm_kernel
+  const unsigned V8 = V & ~7u;
+  unsigned L = b;
+  if (b < V8) {
+    constexpr unsigned XG = 8;
+    const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3, ln = per / XG;
+    L = k < XG * ln ? ((k / ln) * 8u + x) * ln + k % ln : 8u * XG * ln + x * (per - XG * ln) + (k - XG * ln);
+  }
+  const int mt = int(L / unsigned(g.n_ntiles));
+  const int nt = int(L % unsigned(g.n_ntiles));
+  __shared__ uint4 As0[256][16];
+  __shared__ uint4 As1[256][16];
+  const int32_t *tp = g.tiles + 4 * mt;
+  const int e = tp[0], row0 = tp[1], mcount = tp[2];
+  const int c0 = int(blockIdx.z) * g.chunks_per_split;
+  const int c1 = min(c0 + g.chunks_per_split, g.nchunks);
+  const int bits = g.p[0].nbits[e];
+  const int dq = g.dq_mode;
+  const int mb_act = (mcount + 15) >> 4;
+#define MOEQ_W(B, D, M) wide_tile<NB, NP, EPI, ODT, B, D, M>(g, e, row0, mcount, nt, c0, c1, As0, As1)
+#define MOEQ_WM(B, D)                               \
+  if (mb_act <= 2) MOEQ_W(B, D, 2);                 \
+  else if (mb_act <= 4) MOEQ_W(B, D, 4);            \
+  else if (mb_act <= 8) MOEQ_W(B, D, 8);            \
+  else if (mb_act <= 10) MOEQ_W(B, D, 10);          \
+  else MOEQ_W(B, D, 16);
+#define MOEQ_WB(B)                                           \
+  if (dq == MOEQ_DQ_HQQ_INT) { MOEQ_WM(B, MOEQ_DQ_HQQ_INT) } \
+  else if (dq == MOEQ_DQ_HQQ) { MOEQ_WM(B, MOEQ_DQ_HQQ) }    \
+  else { MOEQ_WM(B, MOEQ_DQ_AFFINE) }
+  switch (bits) {
+    case 1: MOEQ_WB(1) break;
+    case 2: MOEQ_WB(2) break;
+    case 3: MOEQ_WB(3) break;
+    default: MOEQ_WB(4) break;
+  }
+#undef MOEQ_WB
+#undef MOEQ_WM
+#undef MOEQ_W
+}
+
+}  // namespace moeq

@@ -31,7 +31,7 @@ def _bm_for_rows(m):
 
 # Largest 16-row block count of a tile class and the next lower count the
 # grouped GEMM has a variant for (tile_rows / tile_blocks_below in csrc/common.h).
-_BLOCKS = {16: (2, 1), 32: (3, 2), 64: (6, 4), 128: (10, 8), 256: (16, 8)}
+_BLOCKS = {16: (2, 1), 32: (3, 2), 64: (6, 4), 128: (10, 8), 256: (16, 10)}
 
 
 def split_rows(m, bm):

@@ -183,7 +183,7 @@ def test_tile_split_rule():
     rows at 16-row boundaries, and never run more 16-row blocks (rounded up to
     the kernel's variants) than an even split of the rows would."""
     from robustgemq_amd.linear import split_rows
-    variants = {16: (1, 2), 32: (2, 3), 64: (2, 4, 6), 128: (2, 4, 8, 10), 256: (2, 4, 8, 16)}
+    variants = {16: (1, 2), 32: (2, 3), 64: (2, 4, 6), 128: (2, 4, 8, 10), 256: (2, 4, 8, 10, 16)}
 
     def run_blocks(rows, bm):
         b = -(-rows // 16)
