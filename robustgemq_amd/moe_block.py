@@ -156,10 +156,23 @@ class _QuantFusedMoEBase(nn.Module):
         return True if self._always_renorm else bool(self.norm_topk_prob)
 
     @classmethod
-    def from_hf(cls, config, hf_block):
-        """Stack the GemLite-converted expert linears of an HF block
-        (moe_block.py:715-761 and family variants).  Weights dequantize as
-        q * s + z' (GemLite zeros), like the reference kernels."""
+    def from_hf(cls, config, hf_block, bits=None, group_size=None, shared_bits=None):
+        """Build the block from an HF MoE block (patch.py:86-162 calls this
+        for every MoE layer).  Two layouts:
+
+        * experts as a list of per-expert modules whose linears are already
+          GemLite-converted (transformers 4.x, the reference's from_hf,
+          moe_block.py:715-761 and family variants): their packed words are
+          stacked and dequantize as q * s + z', like the reference kernels;
+        * experts as one module with 3-D parameters (transformers 5.x:
+          experts.gate_up_proj [E, 2F, H], experts.down_proj [E, H, F], and
+          DeepSeek's shared_experts MLP): every expert slice is quantized here
+          with the RTN rule (gemq/quantizers/rtn.py:15-55) at `bits` (one
+          int, or one per expert), `group_size` and `shared_bits`, and the
+          block computes with the fake-quant weights (q - z) * s, as
+          from_quantized does."""
+        if hasattr(hf_block.experts, "gate_up_proj"):
+            return cls._from_fused_experts(config, hf_block, bits, group_size, shared_bits)
         block = cls(config)
         experts = cls._hf_experts(hf_block)
         n1, n3, n2 = cls._proj_names
@@ -179,6 +192,39 @@ class _QuantFusedMoEBase(nn.Module):
         w2 = _projection(parts[n2], Fd, H, g, L.DQ_AFFINE)
         act = hf_block.gate.weight.dtype if hf_block.gate.weight.dtype != torch.float32 else torch.float16
         return block._install(w1, w3, w2, hf_block.gate.weight.data, act, shared=n_sh)
+
+    @classmethod
+    def _from_fused_experts(cls, config, hf_block, bits, group_size, shared_bits):
+        """transformers 5.x layout: gate_up_proj[e] holds gate_proj (rows
+        0..F-1) over up_proj (rows F..2F-1), as OlmoeExperts.forward splits
+        it with .chunk(2)."""
+        from .quantize import rtn_quantize
+        ex = hf_block.experts
+        E, F2, H = ex.gate_up_proj.shape
+        F = F2 // 2
+        if bits is None or group_size is None:
+            raise ValueError("a block with fused 3-D expert weights is quantized here: pass bits and group_size")
+        bl = [int(bits)] * E if isinstance(bits, int) else [int(b) for b in bits]
+        if len(bl) != E:
+            raise ValueError(f"bits lists {len(bl)} experts, the block has {E}")
+        g = int(group_size)
+        gu_all, dn_all = ex.gate_up_proj.data, ex.down_proj.data
+        experts = []
+        for e in range(E):
+            gu = gu_all[e].to(torch.float16)
+            experts.append({"gate_proj": rtn_quantize(gu[:F].contiguous(), bl[e], g),
+                            "up_proj": rtn_quantize(gu[F:].contiguous(), bl[e], g),
+                            "down_proj": rtn_quantize(dn_all[e].to(torch.float16).contiguous(), bl[e], g)})
+        shared = None
+        sh = getattr(hf_block, "shared_experts", None)
+        if sh is not None:
+            if shared_bits is None:
+                raise ValueError("the block has shared experts: pass shared_bits")
+            shared = {n: rtn_quantize(getattr(sh, n).weight.data.to(torch.float16).contiguous(), int(shared_bits), g)
+                      for n in ("gate_proj", "up_proj", "down_proj")}
+        gw = hf_block.gate.weight.data
+        act = gw.dtype if gw.dtype != torch.float32 else torch.float16
+        return cls.from_quantized(config, gw, experts, shared=shared, act_dtype=act)
 
     @classmethod
     def from_quantized(cls, config, gate_weight, experts, shared=None, act_dtype=torch.float16):
@@ -306,9 +352,9 @@ class QuantFusedDeepseekV2MoEBlock(_QuantFusedMoEBase):
         self.norm_topk_prob = config.norm_topk_prob
 
     @classmethod
-    def from_hf(cls, config, hf_block):
+    def from_hf(cls, config, hf_block, bits=None, group_size=None, shared_bits=None):
         check_deepseek_gate_matches(config, hf_block)
-        return super().from_hf(config, hf_block)
+        return super().from_hf(config, hf_block, bits=bits, group_size=group_size, shared_bits=shared_bits)
 
     def _hf_shared_parts(self, config, hf_block, g):
         sh = hf_block.shared_experts

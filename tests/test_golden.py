@@ -30,6 +30,23 @@ def test_oracle_reproduces_golden():
             np.testing.assert_array_equal(fresh[key], GOLD[key], err_msg=key)
 
 
+def test_hf_level2_golden_regenerates():
+    """tests/golden/hf_level2.npz is what make_hf_level2.py writes: the seeded
+    inputs bit for bit, the stock transformers blocks' float32 outputs within
+    BLAS summation-order noise."""
+    pytest.importorskip("transformers")
+    from golden import make_hf_level2 as mk
+    gold = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hf_level2.npz"))
+    for family in ("olmoe", "mixtral"):
+        x = mk.inputs(family)
+        np.testing.assert_array_equal(gold[f"{family}_x"], x.numpy())
+        ref = mk.reference_block(family, mk.hf_block(family, mk.config(family)))
+        with torch.no_grad():
+            y = ref(x[:mk.T].float().reshape(1, mk.T, mk.H))
+        y = (y[0] if isinstance(y, tuple) else y).reshape(mk.T, mk.H).numpy()
+        np.testing.assert_allclose(y, gold[f"{family}_prefill"], rtol=1e-4, atol=1e-6)
+
+
 def test_block_inputs_regenerate_bit_exact():
     gate, experts, x = mg.block_inputs()
     assert bytes(GOLD["block_sha256"]).hex() == mg.digest(gate, experts, x)
