@@ -15,11 +15,24 @@
 // The MFMAs are written as inline asm with "+a" accumulator operands, the one
 // way to keep the compiler from staging accumulators through VGPRs (with the
 // builtin it parks them in AGPRs as spill slots and copies them back and
-// forth).  The compiler therefore does not see them as MFMAs, and the hazards
-// it would otherwise resolve are handled here:
+// forth).
+//
+// Issue order.  With one wave per SIMD nothing fills the MFMA pipe's gaps but
+// the wave itself.  Measured on gfx950 (16x16x32 f16, one wave per SIMD):
+// back-to-back MFMAs issue every 18 cycles, and up to two independent VALU
+// instructions between consecutive MFMAs cost nothing, while a third doubles
+// the gap.  So every MFMA is fenced by a scheduling barrier and the step's
+// unpacking is cut into single instructions (pair_op) dealt evenly over the
+// gaps: OPS = pairs x ops-per-pair over MBA * NP * NB MFMAs, one instruction
+// per gap for 1/2/4-bit codes at 16 row blocks.
+//
+// Hazards the compiler cannot see, since it does not know the asm is an MFMA:
 //   * a VALU write of a VGPR followed by an MFMA reading it needs two wait
-//     states: every MFMA is preceded by s_nop 1 (the B fragments are VALU
-//     results; the accumulators' zero initialisation is a VALU write too);
+//     states.  MFMA sources are A fragments (LDS loads) and the B fragments
+//     of the previous step; the last unpacking instruction of a step may
+//     directly precede the next step's first MFMA, so each step starts with
+//     s_nop 1 (which also covers copies the compiler places at the loop's
+//     back edge, and the accumulators' zero initialisation);
 //   * an MFMA's result read by a VALU instruction (the epilogue's AGPR reads)
 //     needs the MFMA's passes plus a few wait states: the k loop ends with 24
 //     wait states behind scheduling barriers;
@@ -35,7 +48,66 @@
 namespace moeq {
 
 __device__ __forceinline__ void mfma_agpr(f32x4 &acc, const f16x8 &a, const f16x8 &b) {
-  asm("s_nop 1\n\tv_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// Unpacking one pair of codes (deq_pair's arithmetic) as a sequence of single
+// VALU instructions: the code pair ORed into the mantissa of 1024 (2 ops; 4
+// for 3-bit codes, whose high bit sits in a third word), then the dequant
+// mode's 2 or 3 ops.  pair_op(k) runs op k; the result lands in B[2d..2d+1].
+template <int BITS>
+constexpr int magic_ops() { return BITS == 3 ? 4 : 2; }
+template <int DQ>
+constexpr int deq_ops() { return DQ == MOEQ_DQ_HQQ ? 3 : 2; }
+
+struct PairState {
+  uint32_t x, m;
+  f16x2 v;
+};
+
+template <int BITS, int DQ>
+__device__ __forceinline__ void pair_op(int k, PairState &st, const uint32_t (&w)[BITS], uint32_t sz, int t, int d,
+                                        f16x8 &B) {
+  constexpr uint32_t magic = 0x64006400u;
+  const f16 sh = __builtin_bit_cast(f16, uint16_t(sz & 0xffffu));
+  const f16 zh = __builtin_bit_cast(f16, uint16_t(sz >> 16));
+  const f16x2 s2 = {sh, sh}, z2 = {zh, zh};
+  const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+  constexpr int MO = magic_ops<BITS>();
+  if (k < MO) {
+    if constexpr (BITS == 4) {
+      if (k == 0) st.x = w[t] >> (4 * d);
+      else st.m = and_or(st.x, 0x000f000fu, magic);
+    } else if constexpr (BITS == 2) {
+      if (k == 0) st.x = w[t >> 1] >> (8 * (t & 1) + 2 * d);
+      else st.m = and_or(st.x, 0x00030003u, magic);
+    } else if constexpr (BITS == 1) {
+      if (k == 0) st.x = w[0] >> (4 * t + d);
+      else st.m = and_or(st.x, 0x00010001u, magic);
+    } else {
+      const int hb = 4 * t + d;
+      if (k == 0) st.x = w[t >> 1] >> (8 * (t & 1) + 2 * d);
+      else if (k == 1) st.m = and_or(st.x, 0x00030003u, magic);
+      else if (k == 2) st.x = hb >= 2 ? (w[2] >> (hb - 2)) : (w[2] << (2 - hb));
+      else st.m = and_or(st.x, 0x00040004u, st.m);
+    }
+    return;
+  }
+  const int j = k - MO;
+  f16x2 r;
+  if constexpr (DQ == MOEQ_DQ_HQQ_INT) {
+    if (j == 0) { st.v = __builtin_bit_cast(f16x2, st.m) + z2; return; }
+    r = st.v * s2;
+  } else if constexpr (DQ == MOEQ_DQ_HQQ) {
+    if (j == 0) { st.v = __builtin_bit_cast(f16x2, st.m) - k1024; return; }
+    if (j == 1) { st.v = st.v + z2; return; }
+    r = st.v * s2;
+  } else {
+    if (j == 0) { st.v = __builtin_bit_cast(f16x2, st.m) - k1024; return; }
+    r = __builtin_elementwise_fma(st.v, s2, z2);
+  }
+  B[2 * d] = r[0];
+  B[2 * d + 1] = r[1];
 }
 
 template <int NB, int NP, int EPI, int ODT, int BITS, int DQ, int MBA>
@@ -113,13 +185,15 @@ __device__ __forceinline__ void wide_tile(const GemmArgs &g, int e, int row0, in
 
   uint32_t w0[NP][NB][BITS], w1[NP][NB][BITS], s0[NP][NB], s1[NP][NB];
   f16x8 Bc[NP][NB];
-  // Each MFMA step runs as MBA regions, one per row block, fenced by
-  // scheduling barriers so the work stays spread out: the row block's NP * NB
-  // MFMAs, an even share of the next step's unpacking (NP * NB * 4 pairs per
-  // step), and the LDS read of the A fragment two row blocks ahead (into the
-  // next step while the chunk lasts; a chunk's first two are read after its
-  // barrier).
-  constexpr int PAIRS = NP * NB * 4;
+  // Each MFMA step issues its MBA * NP * NB MFMAs one per scheduling
+  // region; region i also carries ops [i * OPS / S, (i + 1) * OPS / S) of the
+  // next step's unpacking (NP * NB * 4 pairs, in order) and, at the start of
+  // each row block, the LDS read of the A fragment two row blocks ahead (into
+  // the next step while the chunk lasts; a chunk's first two are read after
+  // its barrier).
+  constexpr int S = MBA * NP * NB;
+  constexpr int NOPS = magic_ops<BITS>() + deq_ops<DQ>();
+  constexpr int OPS = NP * NB * 4 * NOPS;
   auto chunk = [&](int c, uint4 (*Ard)[16], uint4 (*Awr)[16], const uint32_t (&wc)[NP][NB][BITS],
                    const uint32_t (&sc)[NP][NB], uint32_t (&wn)[NP][NB][BITS], uint32_t (&sn)[NP][NB]) {
     // next chunk fetched unconditionally (the last chunk re-reads itself)
@@ -134,24 +208,30 @@ __device__ __forceinline__ void wide_tile(const GemmArgs &g, int e, int row0, in
     if constexpr (MBA > 1) Aq[1] = read_a(0, 1);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      // the previous step's last unpacking op may write a B fragment this
+      // step's first MFMA reads: two wait states
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 1");
+      __builtin_amdgcn_sched_barrier(0);
       f16x8 Bn[NP][NB];
+      PairState st[NP * NB * 4];
 #pragma unroll
-      for (int mb = 0; mb < MBA; ++mb) {
-        const int q = t * MBA + mb + 2;  // fragment read two row blocks ahead
-        if (q < 4 * MBA) Aq[q] = read_a(q / MBA, q % MBA);
-#pragma unroll
-        for (int j = mb * PAIRS / MBA; j < (mb + 1) * PAIRS / MBA; ++j) {
-          const int f = j >> 2, d = j & 3, p = f / NB, nb = f % NB;
-          const f16x2 o = t < 3 ? deq_pair<BITS, DQ>(wc[p][nb], sc[p][nb], t + 1, d)
-                                : deq_pair<BITS, DQ>(wn[p][nb], sn[p][nb], 0, d);
-          Bn[p][nb][2 * d] = o[0];
-          Bn[p][nb][2 * d + 1] = o[1];
+      for (int i = 0; i < S; ++i) {
+        const int mb = i / (NP * NB), f = i % (NP * NB), p = f / NB, nb = f % NB;
+        if (f == 0) {
+          const int q = t * MBA + mb + 2;  // fragment read two row blocks ahead
+          if (q < 4 * MBA) Aq[q] = read_a(q / MBA, q % MBA);
         }
-        const f16x8 A = Aq[t * MBA + mb];
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) mfma_agpr(acc[p][mb][nb], A, Bc[p][nb]);
+        for (int o = i * OPS / S; o < (i + 1) * OPS / S; ++o) {
+          const int j = o / NOPS, k = o % NOPS;
+          const int fj = j >> 2, d = j & 3, pj = fj / NB, nbj = fj % NB;
+          if (t < 3)
+            pair_op<BITS, DQ>(k, st[j], wc[pj][nbj], sc[pj][nbj], t + 1, d, Bn[pj][nbj]);
+          else
+            pair_op<BITS, DQ>(k, st[j], wn[pj][nbj], sn[pj][nbj], 0, d, Bn[pj][nbj]);
+        }
+        mfma_agpr(acc[p][mb][nb], Aq[t * MBA + mb], Bc[p][nb]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
