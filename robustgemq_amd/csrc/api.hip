@@ -254,6 +254,11 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   if (rc) return rc;
   if (ev1 && (rc = hip_ok(hipEventRecord(ev1, as_stream(stream)), "moe: event record"))) return rc;
 
+  // one token: down projection and combine in one launch
+  if (T == 1 && m->top_k + m->n_shared <= 32)
+    return launch_down_combine1(&m->w2, static_cast<const uint16_t *>(at(p.off_h)), tiles, inv, w, m->top_k,
+                                m->n_shared, out, out_dtype, as_stream(stream));
+
   moeq_gemm dn = gu;
   dn.a = at(p.off_h);
   dn.a_dtype = MOEQ_F16;

@@ -542,6 +542,12 @@ template <> struct Shape<256, false> { static constexpr int NW = 4, NB = 4; };
 // launches of at most 16 rows per tile skip the two-block kernel path.
 int grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, void *stream);
 
+// One-token forwards: the down projection of the k routed rows plus the
+// shared rows and the weighted combine in one launch (decode1.hip), given
+// the one-token grouping (tiles, inv_perm, w) and the SiLU * up rows h.
+int launch_down_combine1(const moeq_proj *w2, const uint16_t *h, const int32_t *tiles, const int32_t *inv_perm,
+                         const float *w, int k, int n_shared, void *out, int out_dtype, hipStream_t s);
+
 // Launches one configuration (defined in gemm_bm<BM>.hip).
 template <int BM>
 int launch_grouped_gemm(const GemmArgs &g, bool silu, int a_dtype, int out_dtype, int max_tiles, int splits,
