@@ -13,7 +13,7 @@ static int launch_wide(const GemmArgs &g0, int max_tiles, int splits, hipStream_
   const int64_t blocks = int64_t(max_tiles) * g.n_ntiles;
   if (blocks > 0x7fffffff) return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: grid too large");
   dim3 grid(unsigned(blocks), 1, unsigned(splits)), block(S::NW * 64);
-  wide_gemm_kernel<S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ODT><<<grid, block, 0, s>>>(g);
+  wide_gemm_kernel<S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ODT, 16, 1><<<grid, block, 0, s>>>(g);
   return check_launch("grouped_gemm");
 }
 

@@ -115,7 +115,6 @@ __device__ __forceinline__ void wide_tile(const GemmArgs &g, int e, int row0, in
                                           uint4 (*As0)[16], uint4 (*As1)[16]) {
   constexpr int NW = 4, NT = NW * 64;
   static_assert(MBA <= 16, "a wave holds at most 16 row blocks");
-  static_assert(NP * NB * MBA * 4 <= 256, "accumulators exceed the AGPRs");
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, kb = lane >> 4;
@@ -300,9 +299,12 @@ __device__ __forceinline__ void wide_tile(const GemmArgs &g, int e, int row0, in
   }
 }
 
-// One work-group of four waves per CU; the LDS holds two 64 KB A buffers.
-template <int NB, int NP, int EPI, int ODT>
-__global__ __launch_bounds__(256, 1) void wide_gemm_kernel(GemmArgs g) {
+// Four waves per work-group and OCC work-groups per CU (OCC waves per SIMD,
+// 512 / OCC registers each); tiles of up to MAXB row blocks, whose two A
+// buffers take 2 * MAXB * 4 KB of LDS.
+template <int NB, int NP, int EPI, int ODT, int MAXB, int OCC>
+__global__ __launch_bounds__(256, OCC) void wide_gemm_kernel(GemmArgs g) {
+  static_assert(NP * NB * MAXB * 4 <= 256 / OCC, "accumulators exceed the AGPRs of a wave");
   const unsigned V = unsigned(*g.n_tiles) * unsigned(g.n_ntiles);
   const unsigned b = blockIdx.x;
   if (b >= V) return;
@@ -316,8 +318,8 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(GemmArgs g) {
   }
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
-  __shared__ uint4 As0[256][16];
-  __shared__ uint4 As1[256][16];
+  __shared__ uint4 As0[MAXB * 16][16];
+  __shared__ uint4 As1[MAXB * 16][16];
   const int32_t *tp = g.tiles + 4 * mt;
   const int e = tp[0], row0 = tp[1], mcount = tp[2];
   const int c0 = int(blockIdx.z) * g.chunks_per_split;
@@ -326,12 +328,20 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(GemmArgs g) {
   const int dq = g.dq_mode;
   const int mb_act = (mcount + 15) >> 4;
 #define MOEQ_W(B, D, M) wide_tile<NB, NP, EPI, ODT, B, D, M>(g, e, row0, mcount, nt, c0, c1, As0, As1)
-#define MOEQ_WM(B, D)                               \
-  if (mb_act <= 2) MOEQ_W(B, D, 2);                 \
-  else if (mb_act <= 4) MOEQ_W(B, D, 4);            \
-  else if (mb_act <= 8) MOEQ_W(B, D, 8);            \
-  else if (mb_act <= 10) MOEQ_W(B, D, 10);          \
-  else MOEQ_W(B, D, 16);
+#define MOEQ_WM(B, D)                                                   \
+  if constexpr (MAXB == 16) {                                           \
+    if (mb_act <= 2) MOEQ_W(B, D, 2);                                   \
+    else if (mb_act <= 4) MOEQ_W(B, D, 4);                              \
+    else if (mb_act <= 8) MOEQ_W(B, D, 8);                              \
+    else if (mb_act <= 10) MOEQ_W(B, D, 10);                            \
+    else MOEQ_W(B, D, 16);                                              \
+  } else {                                                              \
+    static_assert(MAXB == 8, "row-block variants for 8 or 16 blocks");  \
+    if (mb_act <= 2) MOEQ_W(B, D, 2);                                   \
+    else if (mb_act <= 4) MOEQ_W(B, D, 4);                              \
+    else if (mb_act <= 6) MOEQ_W(B, D, 6);                              \
+    else MOEQ_W(B, D, 8);                                               \
+  }
 #define MOEQ_WB(B)                                           \
   if (dq == MOEQ_DQ_HQQ_INT) { MOEQ_WM(B, MOEQ_DQ_HQQ_INT) } \
   else if (dq == MOEQ_DQ_HQQ) { MOEQ_WM(B, MOEQ_DQ_HQQ) }    \
