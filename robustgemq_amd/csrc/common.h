@@ -43,6 +43,13 @@ __host__ __device__ constexpr int tile_blocks_below(int bm) {
   return bm == 16 ? 1 : bm == 32 ? 2 : bm == 64 ? 4 : bm == 128 ? 8 : bm == 256 ? 10 : 0;
 }
 
+// The variant below tile_blocks_below(bm) (0 where that is the smallest):
+// the schedule lists tiles of more blocks than tile_blocks_below first, then
+// those of more than this, then the rest.
+__host__ __device__ constexpr int tile_blocks_below2(int bm) {
+  return bm == 64 ? 2 : bm == 128 ? 4 : bm == 256 ? 8 : 0;
+}
+
 // ------------------------------------------------------- device helpers
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(uint32_t(b) << 16);

@@ -410,6 +410,52 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
   char *const tile_out =
       static_cast<char *>(g.out) + (int64_t(blockIdx.z) * g.split_stride + int64_t(row0) * g.ldo) * OES;
   const uint32_t lane_off = uint32_t(4 * kb) * uint32_t(ldo_b) + uint32_t((n_wave + l16) * OES);
+  if constexpr (BM >= 32 && OES == 2) {
+    // Prefill tiles with 16-bit outputs go out through LDS: the waves leave
+    // their fp16 results in the two A buffers (row r of the tile at row
+    // r % RPB of buffer r / RPB, 16-byte units XOR-swizzled by (r / 4) % 4 so
+    // the four row groups of one store hit disjoint banks), then every thread
+    // writes whole 16-byte row pieces, so each row's columns leave as full
+    // cache lines instead of 2-byte stores per accumulator.  Needs 16-byte
+    // aligned output rows (the layer's h and y are).
+    constexpr int COLS = NW * NB * 16;
+    constexpr int UPR = COLS / 8;                    // 16-byte units per staged row
+    constexpr int RPB = tile_rows(BM) * 128 / COLS;  // staged rows per A buffer
+    static_assert(UPR >= 8 && (UPR & (UPR - 1)) == 0, "staged rows: a power of two of at least 8 units");
+    static_assert(2 * RPB >= MBA * 16, "staged tile exceeds the A buffers");
+    if (((reinterpret_cast<uintptr_t>(tile_out) | uintptr_t(ldo_b)) & 15) == 0) {
+      // the last chunk's repeated prefetch may still be landing in a buffer
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      char *const sb0 = reinterpret_cast<char *>(&As0[0][0]);
+      char *const sb1 = reinterpret_cast<char *>(&As1[0][0]);
+      auto srow = [&](int r) { return r < RPB ? sb0 + r * (COLS * 2) : sb1 + (r - RPB) * (COLS * 2); };
+      auto swz = [](int r) { return ((r >> 2) & 3) << 1; };
+      const int cw = wave * NB * 16;  // the wave's first column in the tile
+#pragma unroll
+      for (int mb = 0; mb < MBA; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mb + 4 * kb + i, c = cw + nb * 16 + l16;
+            uint16_t v;
+            if constexpr (EPI == MOEQ_EPI_SILU_MUL) v = f32_to_f16_bits(silu_mul(acc[0][mb][nb][i], acc[NP - 1][mb][nb][i]));
+            else v = f32_to_f16_bits(acc[0][mb][nb][i]);
+            *reinterpret_cast<uint16_t *>(srow(r) + (((c >> 3) ^ swz(r)) << 4) + (c & 7) * 2) = v;
+          }
+      __syncthreads();
+      const int rows = min(MBA * 16, mcount);
+      const int col0 = nt * COLS;
+      for (int q = int(threadIdx.x); q < rows * UPR; q += NT) {
+        const int r = q / UPR, u = q % UPR, col = col0 + u * 8;
+        if (col < N)
+          *reinterpret_cast<uint4 *>(tile_out + int64_t(r) * ldo_b + col * 2) =
+              *reinterpret_cast<const uint4 *>(srow(r) + ((u ^ swz(r)) << 4));
+      }
+      return;
+    }
+  }
   auto put = [&](int mb, int nb, int i) {
     char *p = tile_out + int64_t(16 * mb + i) * ldo_b + (lane_off + uint32_t(nb * 16 * OES));
     if constexpr (EPI == MOEQ_EPI_SILU_MUL) {
@@ -463,31 +509,35 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
 #undef MOEQ_T
 }
 
+// Block b of a launch of V live blocks -> block L of the tile list (tile
+// L / n_ntiles, column tile L % n_ntiles).  Work-groups are dealt to the 8
+// XCDs round-robin, so XCD x = b % 8 takes its k-th block as block L: the
+// list (first V8 = V & ~7 blocks) is cut into 8 * XG segments of ln blocks,
+// ln one row tile's column tiles (at most an eighth of an XCD's share), and
+// XCD x gets segments x, x + 8, x + 16, ... (XG of them).  The schedule lists
+// the largest tiles first, so every XCD starts its longest tiles first and
+// gets an even share of each tile size, while a segment keeps a row tile's
+// column tiles (which read the same activation rows) on one L2; the
+// per % XG blocks left over go to the XCDs as equal runs after the segments.
+__device__ __forceinline__ unsigned xcd_block(unsigned b, unsigned V, unsigned n_ntiles) {
+  const unsigned V8 = V & ~7u;
+  if (b >= V8) return b;
+  const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3;
+  const unsigned ln = max(1u, min(n_ntiles, per / 8u)), XG = per / ln;
+  return k < XG * ln ? ((k / ln) * 8u + x) * ln + k % ln : 8u * XG * ln + x * (per - XG * ln) + (k - XG * ln);
+}
+
 // Two work-groups per CU for the 32..128 classes (tiles of up to 48..160
 // rows): 2 waves per SIMD.
 template <int BM, int NW, int NB, int NP, int EPI, int ADT, int ODT, bool KS, bool MB2 = true>
 __global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel(GemmArgs g) {
   // The grid is sized for the host-side bound on row tiles; blocks past the
-  // real count (read from the device schedule) exit together.  Work-groups
-  // are dealt to the 8 XCDs round-robin, so the live ones are renumbered to
-  // give each XCD runs of neighbouring tiles (same row tile with neighbouring
-  // column tiles, then the next row tile of the same expert) sharing its L2.
+  // real count (read from the device schedule) exit together; the live ones
+  // are renumbered per XCD (xcd_block).
   const unsigned V = unsigned(*g.n_tiles) * unsigned(g.n_ntiles);
   const unsigned b = blockIdx.x;
   if (b >= V) return;
-  // XCD x = b % 8 takes its k-th block as block L of the tile list: the list
-  // (first V8 = V & ~7 blocks) is cut into 8 * XG segments of ln blocks and
-  // XCD x gets segments x, x + 8, x + 16, ... (XG of them), so tiles of
-  // different sizes (Zipf routing, remainder tiles) spread over the XCDs
-  // while each segment keeps neighbouring tiles together; the per % XG blocks
-  // left over go to the XCDs as equal runs after the segments.
-  const unsigned V8 = V & ~7u;
-  unsigned L = b;
-  if (b < V8) {
-    constexpr unsigned XG = 8;
-    const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3, ln = per / XG;
-    L = k < XG * ln ? ((k / ln) * 8u + x) * ln + k % ln : 8u * XG * ln + x * (per - XG * ln) + (k - XG * ln);
-  }
+  const unsigned L = xcd_block(b, V, unsigned(g.n_ntiles));
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
   // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * MBA *

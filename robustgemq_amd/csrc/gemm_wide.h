@@ -308,14 +308,7 @@ __global__ __launch_bounds__(256, OCC) void wide_gemm_kernel(GemmArgs g) {
   const unsigned V = unsigned(*g.n_tiles) * unsigned(g.n_ntiles);
   const unsigned b = blockIdx.x;
   if (b >= V) return;
-  // XCD-aware renumbering, as grouped_gemm_kernel
-  const unsigned V8 = V & ~7u;
-  unsigned L = b;
-  if (b < V8) {
-    constexpr unsigned XG = 8;
-    const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3, ln = per / XG;
-    L = k < XG * ln ? ((k / ln) * 8u + x) * ln + k % ln : 8u * XG * ln + x * (per - XG * ln) + (k - XG * ln);
-  }
+  const unsigned L = xcd_block(b, V, unsigned(g.n_ntiles));
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
   __shared__ uint4 As0[MAXB * 16][16];

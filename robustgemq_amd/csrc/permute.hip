@@ -87,6 +87,35 @@ __device__ int block_exclusive_scan(int v, int *sh, int *total) {
   return r;
 }
 
+// The same over one packed 64-bit value per thread (three 21-bit counts).
+__device__ uint64_t block_exclusive_scan64(uint64_t v, uint64_t *sh, uint64_t *total) {
+  const int lane = lane_id(), w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  uint64_t incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) sh[w] = incl;
+  __syncthreads();
+  if (w == 0) {
+    const uint64_t tv = lane < nw ? sh[lane] : 0;
+    uint64_t ti = tv;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t t = __shfl_up(ti, o);
+      if (lane >= o) ti += t;
+    }
+    if (lane < nw) sh[lane] = ti - tv;
+    if (lane == nw - 1) sh[16] = ti;
+  }
+  __syncthreads();
+  const uint64_t r = sh[w] + incl - v;
+  *total = sh[16];
+  __syncthreads();
+  return r;
+}
+
 // Given per-expert row counts (one per thread e < Et), writes counts,
 // offsets, the tile schedule and the shared-expert rows; returns this
 // expert's first row.  Every thread of the block must call it.
@@ -95,9 +124,8 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
                         int32_t *n_tiles, int *sh, int *s_off) {
   const int e = threadIdx.x, Et = E + n_shared;
   const int m = e < Et ? c : 0;
-  // An expert's rows in ceil(m / cap) tiles cut at 16-row block boundaries;
-  // experts in order, so the tiles sharing an expert's weights are dispatched
-  // together.  A tile of b blocks runs the kernel variant with the smallest
+  // An expert's rows in ceil(m / cap) tiles cut at 16-row block boundaries.
+  // A tile of b blocks runs the kernel variant with the smallest
   // block count >= b, so the first x tiles take the class's largest count
   // smax and the rest the next lower count s2, x being the fewest that hold
   // all B blocks: an expert of 17 blocks at smax = 10 runs 10 + 8 = 18
@@ -107,9 +135,31 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
   const int B = (m + 15) / 16;
   const int nt = (B + smax - 1) / smax;
   const int x = smax == s2 ? nt : min(nt, max(0, (B - s2 * nt + (smax - s2) - 1) / (smax - s2)));
-  int tot_rows, tot_tiles;
+  // The list runs by kernel variant, largest first: class 0 = tiles of more
+  // than s2 blocks (the largest variant), class 1 = more than the variant
+  // below s2, class 2 = the rest; experts in order within a class.  An
+  // expert's classes never decrease along its tiles, so its tiles keep their
+  // order; the dispatcher starts the longest tiles first and the short ones
+  // fill the end of the launch.
+  const int below = tile_blocks_below2(bm);
+  auto tile_blocks = [&](int j, int &b0) {
+    b0 = j < x ? j * smax : x * smax + (j - x) * s2;
+    return min(b0 + (j < x ? smax : s2), B) - b0;
+  };
+  auto cls = [&](int nb) { return nb > s2 ? 0 : nb > below ? 1 : 2; };
+  uint64_t mine = 0;
+  for (int j = 0; j < nt; ++j) {
+    int b0;
+    mine += uint64_t(1) << (21 * cls(tile_blocks(j, b0)));
+  }
+  __shared__ uint64_t sh64[17];
+  int tot_rows;
+  uint64_t tot_cls;
   const int off = block_exclusive_scan(m, sh, &tot_rows);
-  const int tb = block_exclusive_scan(nt, sh, &tot_tiles);
+  const uint64_t before = block_exclusive_scan64(mine, sh64, &tot_cls);
+  constexpr uint64_t kF = (uint64_t(1) << 21) - 1;
+  const int t0 = int(tot_cls & kF), t1 = int((tot_cls >> 21) & kF), t2 = int(tot_cls >> 42);
+  int pos0 = int(before & kF), pos1 = t0 + int((before >> 21) & kF), pos2 = t0 + t1 + int(before >> 42);
   if (e < Et) {
     counts[e] = c;
     offsets[e] = off;
@@ -119,15 +169,18 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
     offsets[Et] = tot_rows;
     // moeq_max_tiles bounds the count for any routing; the clamp only keeps
     // a corrupted idx from writing past the schedule buffer
-    *n_tiles = min(tot_tiles, max_tiles);
+    *n_tiles = min(t0 + t1 + t2, max_tiles);
   }
-  for (int j = 0; j < nt && tb + j < max_tiles; ++j) {
+  for (int j = 0; j < nt; ++j) {
     // (nt - 1) * smax < B, so every tile before the last is full and the
     // last one holds at least one block
-    const int b0 = j < x ? j * smax : x * smax + (j - x) * s2;
-    const int b1 = min(b0 + (j < x ? smax : s2), B);
-    const int r0 = 16 * b0, r1 = min(16 * b1, m);
-    int32_t *tp = tiles + 4 * (tb + j);
+    int b0;
+    const int nb = tile_blocks(j, b0);
+    const int k = cls(nb);
+    const int at = k == 0 ? pos0++ : k == 1 ? pos1++ : pos2++;
+    if (at >= max_tiles) continue;
+    const int r0 = 16 * b0, r1 = min(16 * (b0 + nb), m);
+    int32_t *tp = tiles + 4 * at;
     tp[0] = e;
     tp[1] = off + r0;
     tp[2] = r1 - r0;
