@@ -48,8 +48,10 @@ extern "C" {
 /* Quantized projection of all experts of one MoE layer, in the build layout
  * written by moeq_repack (codes) and moeq_prep_scales (scale/zero pairs).
  * Per expert e (bits b = nbits[e]) the code block holds K*N*b/32 words
- * starting at words + word_off[e]; the scale/zero block holds (K/group_size)
- * rows of N dwords starting at sz + sz_off[e].  Device arrays. */
+ * starting at words + word_off[e]; the scale/zero block holds
+ * (K/group_size)*N dwords starting at sz + sz_off[e].  Both are panel-major:
+ * panel p = n / 16 holds its 16 columns' data over all of K, so a wave
+ * streaming a panel reads one contiguous run.  Device arrays. */
 typedef struct moeq_proj {
   const uint32_t *words;
   const int64_t *word_off; /* [n_experts] */
@@ -95,20 +97,30 @@ int moeq_pack_cols(const uint8_t *codes, int64_t N, int64_t K, int nbits,
                    int32_t *out, void *stream);
 
 /* Rewrite one expert's reference-layout words [ceil(K/eps), N] (as above) into
- * the build layout (K*N*nbits/32 words).  K % 128 == 0.
+ * the build layout (K*N*nbits/32 words).  K % 128 == 0, N % 16 == 0.
+ * The 32 codes k = 128c + 32kb + i (i = 8t + 2d + h) of column n form the
+ * nbits-word lane slice (c, n, kb), stored at word
+ * ((n/16 * K/128 + c) * 64 + (n%16) * 4 + kb) * nbits; inside it the pair
+ * h = 0, 1 of MFMA step t, pair d sits at one bit offset of the two 16-bit
+ * halves of a word (4-bit: word t, bit 16h+4d; 2-bit: word t/2, bit
+ * 16h+2(4(t%2)+d); 1-bit: word 0, bit 16h+4t+d; 3-bit: the low two bits as
+ * the 2-bit plane in words 0-1, the high bit as the 1-bit plane in word 2).
  * Load-time counterpart of the stacking in from_hf,
  * gemq/inference/moe_block.py:725-757; the reference has no repack step. */
 int moeq_repack(const int32_t *ref_words, int64_t K, int64_t N, int nbits,
                 uint32_t *out, void *stream);
 
-/* Fuse per-group fp16 scale s and zero z ([G, N] each) into half2 dwords:
+/* Fuse per-group fp16 scale s and zero z into half2 dwords:
  * MOEQ_DQ_HQQ -> (s, -z); MOEQ_DQ_AFFINE -> (s, z');
  * MOEQ_DQ_HQQ_INT -> (s, -(1024 + z)), exact for integer z in 0..1023 (the
- * caller checks that).  Element-wise.
+ * caller checks that).  scales/zeros are `blocks` consecutive [groups, N]
+ * arrays (one per expert, the reference's stacking); out has the same size,
+ * each block panel-major: pair (g, n) at dword (n/16 * groups + g) * 16 + n%16
+ * of its block.  N % 16 == 0.
  * Replaces the separate scales/zeros loads of dequantize(),
  * gemq/triton_kernels/utils.py:192-212. */
-int moeq_prep_scales(const uint16_t *scales, const uint16_t *zeros,
-                     int64_t n, int dq_mode, uint32_t *out, void *stream);
+int moeq_prep_scales(const uint16_t *scales, const uint16_t *zeros, int64_t blocks,
+                     int64_t groups, int64_t N, int dq_mode, uint32_t *out, void *stream);
 
 /* ------------------------------------------------------------------ routing */
 
@@ -195,7 +207,7 @@ typedef struct moeq_gemm {
  * p1 must be NULL for MOEQ_EPI_STORE and match p0's layout for SILU_MUL.
  * Every A row the tiles address (row_src[r], or r) must lie wholly within
  * the first 2 GiB from a, i.e. (row + 1) * lda * element size <= 2^31
- * (the LDS-staged tiles address rows with 32-bit offsets; the caller checks
+ * (every tile class addresses rows with 32-bit offsets; the caller checks
  * this, the library cannot see the rows row_src names); one expert's packed
  * words must be < 2 GiB.
  * Replaces the per-expert launches of dequant_group_gemm_triton

@@ -116,7 +116,9 @@ def unpack_cols(words, nbits, K):
 # Codes of column n, reduction index k = 128*c + 32*kb + i (i = 8*t + 2*d + h)
 # sit in the lane slice (c, n, kb), nbits words long, so that for MFMA step t
 # and pair d the two codes (h = 0, 1) land at the same bit offset of the low
-# and high 16-bit halves of one word.
+# and high 16-bit halves of one word.  Slices are stored panel-major: panel
+# p = n // 16 holds chunk 0's slices of its 16 columns, then chunk 1's, ...
+# (order [p][c][n % 16][kb][word]).
 def _slice_bits(nbits):
     """For each i in 0..31 a list of (word, bit, code_shift, width) fields."""
     out = []
@@ -137,14 +139,15 @@ def _slice_bits(nbits):
 
 
 def repack_build(codes, nbits):
-    """uint8 codes [N, K] -> uint32 build-layout words, shape [K/128, N, 4, nbits]
-    (flattened in that order on the device)."""
+    """uint8 codes [N, K] -> uint32 build-layout words, shape
+    [N/16, K/128, 16, 4, nbits] = [panel, c, n % 16, kb, word] (flattened in
+    that order on the device)."""
     codes = np.asarray(codes, dtype=np.uint32)
     N, K = codes.shape
-    assert K % 128 == 0
+    assert K % 128 == 0 and N % 16 == 0
     C = K // 128
-    q = codes.reshape(N, C, 4, 32).transpose(1, 0, 2, 3)  # [c, n, kb, i]
-    out = np.zeros((C, N, 4, nbits), np.uint32)
+    q = codes.reshape(N // 16, 16, C, 4, 32).transpose(0, 2, 1, 3, 4)  # [p, c, n%16, kb, i]
+    out = np.zeros((N // 16, C, 16, 4, nbits), np.uint32)
     for i, fields in enumerate(_slice_bits(nbits)):
         for (w, bit, cshift, width) in fields:
             v = (q[..., i] >> np.uint32(cshift)) & np.uint32((1 << width) - 1)
@@ -153,17 +156,18 @@ def repack_build(codes, nbits):
 
 
 def unpack_build(words, nbits, N, K):
-    """Inverse of repack_build: words [K/128, N, 4, nbits] -> codes [N, K]."""
-    w = np.asarray(words, dtype=np.uint32).reshape(K // 128, N, 4, nbits)
-    q = np.zeros((K // 128, N, 4, 32), np.uint32)
+    """Inverse of repack_build: words [N/16, K/128, 16, 4, nbits] -> codes [N, K]."""
+    w = np.asarray(words, dtype=np.uint32).reshape(N // 16, K // 128, 16, 4, nbits)
+    q = np.zeros((N // 16, K // 128, 16, 4, 32), np.uint32)
     for i, fields in enumerate(_slice_bits(nbits)):
         for (wi, bit, cshift, width) in fields:
             q[..., i] |= ((w[..., wi] >> np.uint32(bit)) & np.uint32((1 << width) - 1)) << np.uint32(cshift)
-    return q.transpose(1, 0, 2, 3).reshape(N, K).astype(np.uint8)
+    return q.transpose(0, 2, 1, 3, 4).reshape(N, K).astype(np.uint8)
 
 
 def prep_scales(s, z, dq_mode):
-    """Per-group (s, z) fp16 arrays of equal shape -> uint32 half2 pairs:
+    """Per-group (s, z) fp16 arrays [G, N] (one expert) -> uint32 half2 pairs
+    in the panel-major build order [N/16, G, 16]:
     HQQ (mode 0): low half s, high half -z; AFFINE (mode 1): s, z';
     HQQ_INT (mode 2, integer z in 0..1023): s, -(1024 + z)."""
     sb = np.asarray(s, dtype=np.float16).view(np.uint16).astype(np.uint32)
@@ -174,7 +178,10 @@ def prep_scales(s, z, dq_mode):
         assert np.all((zz == np.round(zz)) & (zz >= 0) & (zz <= 1023))
         zz = (-(1024.0 + zz.astype(np.float64))).astype(np.float16)
     zb = zz.astype(np.float16).view(np.uint16).astype(np.uint32)
-    return (sb | (zb << 16)).astype(np.uint32)
+    pairs = (sb | (zb << 16)).astype(np.uint32)
+    G, N = pairs.shape
+    assert N % 16 == 0
+    return np.ascontiguousarray(pairs.reshape(G, N // 16, 16).transpose(1, 0, 2))
 
 
 def kernel_dequant_hqq(codes, s_nk, z_nk, group_size):

@@ -83,7 +83,7 @@ SIGNATURES = {
     "moeq_version": (c_int, []),
     "moeq_pack_cols": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "moeq_repack": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
-    "moeq_prep_scales": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
+    "moeq_prep_scales": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "moeq_route_workspace_size": (c_size_t, [c_int64, c_int]),
     "moeq_route": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
                            c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -30,6 +30,7 @@ struct Down1Args {
   const int32_t *inv_perm;  // [k] row of each slot
   const float *w;           // [k] routing weights
   int R, k, K, N, group_size, gshift, dq_mode;
+  uint32_t gmagic;  // ceil(2^32 / group_size)
   ProjDev p;                // down projection
   void *out;
   int out_dtype;
@@ -43,22 +44,26 @@ __device__ __forceinline__ float d1_segment(const Down1Args &a, int r, int cb, i
   const int e = a.tiles[4 * r];
   const char *wb = reinterpret_cast<const char *>(a.p.words + a.p.word_off[e]);
   const char *sb = reinterpret_cast<const char *>(a.p.sz + a.p.sz_off[e]);
-  const uint32_t woff = uint32_t(((n0 + l16) * 4 + kb) * BITS * 4);
-  const uint32_t soff = uint32_t((n0 + l16) * 4);
-  const int64_t chunk_bytes = int64_t(a.N) * 16 * BITS;
-  const uint32_t grp_bytes = uint32_t(a.N) * 4u;
-  const char *arow = reinterpret_cast<const char *>(a.h) + int64_t(r) * a.K * 2;
+  const int groups = a.gshift >= 0 ? a.K >> a.gshift : a.K / a.group_size;
+  const uint32_t woff = slice_byte_off<BITS>(n0 + l16, kb, a.K / 128);
+  const uint32_t soff = sz_byte_off(n0 + l16, groups);
+  constexpr uint32_t chunk_bytes = uint32_t(chunk_step_bytes<BITS>());
+  constexpr uint32_t grp_bytes = kGroupStepBytes;
+  // buffer loads: the lane's 32-bit offset plus the chunk's scalar offset
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wb), srs = buffer_rsrc(sb);
+  const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(reinterpret_cast<const char *>(a.h) + int64_t(r) * a.K * 2);
   const int nc = ce - cb;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   auto fetch = [&](int j, uint4 (&av)[4], uint32_t (&w)[BITS], uint32_t &sz) {
     const int c = cb + min(j, nc - 1);
-    const uint4 *pa = reinterpret_cast<const uint4 *>(arow + (int64_t(c) * 128 + 32 * kb) * 2);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) av[t] = pa[t];
-    load_slice<BITS>(reinterpret_cast<const uint32_t *>(wb + int64_t(c) * chunk_bytes + woff), w);
-    const int k = c * 128 + 32 * kb;
-    const uint32_t grp = uint32_t(a.gshift >= 0 ? k >> a.gshift : k / a.group_size);
-    sz = *reinterpret_cast<const uint32_t *>(sb + (grp * grp_bytes + soff));
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ars, int(64 * kb + 16 * t), c * 256, 0);
+      av[t] = (uint4){v[0], v[1], v[2], v[3]};
+    }
+    load_slice_buf<BITS>(wrs, woff, uint32_t(c) * chunk_bytes, w);
+    const uint32_t grp = __umulhi(uint32_t(c * 128 + 32 * kb), a.gmagic);
+    sz = __builtin_amdgcn_raw_buffer_load_b32(srs, int(soff + grp * grp_bytes), 0, 0);
   };
   auto step = [&](bool live, const uint4 (&av)[4], const uint32_t (&w)[BITS], uint32_t sz) {
 #pragma unroll
@@ -156,6 +161,7 @@ int launch_down_combine1(const moeq_proj *w2, const uint16_t *h, const int32_t *
   a.N = w2->N;
   a.group_size = w2->group_size;
   a.gshift = (w2->group_size & (w2->group_size - 1)) ? -1 : __builtin_ctz(unsigned(w2->group_size));
+  a.gmagic = uint32_t(((uint64_t(1) << 32) + uint64_t(w2->group_size) - 1) / uint64_t(w2->group_size));
   a.dq_mode = w2->dq_mode;
   a.p = ProjDev{w2->words, w2->word_off, w2->sz, w2->sz_off, w2->nbits};
   a.out = out;

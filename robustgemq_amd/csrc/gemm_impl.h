@@ -45,6 +45,9 @@ struct GemmArgs {
   const int32_t *tiles;
   const int32_t *n_tiles;
   int K, N, group_size, gshift, dq_mode;  // gshift = log2(group_size), or -1
+  // group index of reduction index k: umulhi(k, gmagic) = k / group_size
+  // (gmagic = ceil(2^32 / group_size), exact for k * group_size < 2^32)
+  uint32_t gmagic;
   ProjDev p[2];
   void *out;
   int64_t ldo, split_stride;
@@ -117,6 +120,49 @@ __device__ __forceinline__ f16x8 deq_frag(const uint32_t (&w)[BITS], uint32_t sz
   return r;
 }
 
+// Build-layout addressing (moeq_repack, moeq_prep_scales).  Panel p = n / 16
+// holds the lane slices of its 16 columns chunk after chunk: slice (c, n, kb)
+// at word ((p * nchunks + c) * 64 + (n % 16) * 4 + kb) * BITS, so the slices
+// of chunk c + 1 follow those of chunk c (256 * BITS bytes on); the
+// scale/zero pair of group g at dword (p * groups + g) * 16 + n % 16 (64 bytes
+// from one group to the next).  Byte offsets of chunk / group 0; one expert's
+// codes and pairs stay below 2 GiB (checked at launch).
+template <int BITS>
+__device__ __forceinline__ uint32_t slice_byte_off(int n, int kb, int nchunks) {
+  return uint32_t(((int64_t(n >> 4) * nchunks * 64) + (n & 15) * 4 + kb) * BITS * 4);
+}
+template <int BITS>
+constexpr int64_t chunk_step_bytes() { return 256 * BITS; }
+__device__ __forceinline__ uint32_t sz_byte_off(int n, int groups) {
+  return uint32_t((int64_t(n >> 4) * groups * 16 + (n & 15)) * 4);
+}
+constexpr uint32_t kGroupStepBytes = 64;
+
+// A buffer resource over `base` (wave-uniform): loads through it take a
+// 32-bit lane offset and a scalar offset, so no 64-bit lane addresses are
+// formed; offsets past 2 GiB read zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// One lane slice (BITS words) at byte offset voff + soff of a buffer.
+template <int BITS>
+__device__ __forceinline__ void load_slice_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                               uint32_t (&w)[BITS]) {
+  if constexpr (BITS == 4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else if constexpr (BITS == 3) {
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, int(voff), int(soff), 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2];
+  } else if constexpr (BITS == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, int(voff), int(soff), 0);
+    w[0] = v[0]; w[1] = v[1];
+  } else {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), 0);
+  }
+}
+
 template <int BITS>
 __device__ __forceinline__ void load_slice(const uint32_t *p, uint32_t (&w)[BITS]) {
   if constexpr (BITS == 4) {
@@ -173,15 +219,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
     sbase[p] = reinterpret_cast<const char *>(g.p[p].sz + g.p[p].sz_off[e]);
   }
   // columns past N read column N - 1 and are never stored
+  const int groups = g.gshift >= 0 ? g.K >> g.gshift : g.K / g.group_size;
   uint32_t woff[NB], soff[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int ncol = min(n_wave + nb * 16 + l16, N - 1);
-    woff[nb] = uint32_t((ncol * 4 + kb) * BITS * 4);
-    soff[nb] = uint32_t(ncol * 4);
+    woff[nb] = slice_byte_off<BITS>(ncol, kb, g.nchunks);
+    soff[nb] = sz_byte_off(ncol, groups);
   }
-  const int64_t chunk_bytes = int64_t(N) * 16 * BITS;  // words of one 128-deep chunk
-  const uint32_t grp_bytes = uint32_t(N) * 4u;         // one scale/zero row
+  constexpr int64_t chunk_bytes = chunk_step_bytes<BITS>();  // one 128-deep chunk of a panel
+  constexpr uint32_t grp_bytes = kGroupStepBytes;            // one group of a panel
 
   f32x4 acc[NP][MBA][NB];
 #pragma unroll

@@ -128,15 +128,16 @@ __device__ __forceinline__ void wide_tile(const GemmArgs &g, int e, int row0, in
     wbase[p] = reinterpret_cast<const char *>(g.p[p].words + g.p[p].word_off[e]);
     sbase[p] = reinterpret_cast<const char *>(g.p[p].sz + g.p[p].sz_off[e]);
   }
+  const int groups = g.gshift >= 0 ? g.K >> g.gshift : g.K / g.group_size;
   uint32_t woff[NB], soff[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int ncol = min(n_wave + nb * 16 + l16, N - 1);
-    woff[nb] = uint32_t((ncol * 4 + kb) * BITS * 4);
-    soff[nb] = uint32_t(ncol * 4);
+    woff[nb] = slice_byte_off<BITS>(ncol, kb, g.nchunks);
+    soff[nb] = sz_byte_off(ncol, groups);
   }
-  const int64_t chunk_bytes = int64_t(N) * 16 * BITS;
-  const uint32_t grp_bytes = uint32_t(N) * 4u;
+  constexpr int64_t chunk_bytes = chunk_step_bytes<BITS>();
+  constexpr uint32_t grp_bytes = kGroupStepBytes;
 
   f32x4 acc[NP][MBA][NB];
 #pragma unroll

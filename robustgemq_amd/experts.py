@@ -9,8 +9,9 @@ each expert's GemLite tensors into
 and builds int32 [E] meta tensors nbits, group_sizes and the exclusive
 cumsums wq_strides / zs_strides.  QuantProjection keeps exactly those (so code
 that pokes the attributes keeps working) and, once at load time, derives
-    words    build-layout codes (moeq_repack), word_off [E] int64
-    sz       fused (scale, zero) half2 pairs (moeq_prep_scales), sz_off [E]
+    words    build-layout codes (moeq_repack, panel-major), word_off [E] int64
+    sz       fused (scale, zero) half2 pairs (moeq_prep_scales, panel-major),
+             sz_off [E]
 """
 
 import ctypes
@@ -96,8 +97,9 @@ class QuantProjection:
                 # integer zero points: one fp16 op less per weight pair, same weights
                 dq_mode = L.DQ_HQQ_INT
         self.dq_mode = dq_mode
-        self.sz = torch.empty(self.scales.shape, dtype=torch.int32, device=dev)
-        L.check(lib.moeq_prep_scales(L.ptr(self.scales), L.ptr(self.zeros), self.scales.numel(), dq_mode,
+        G = K // group_size
+        self.sz = torch.empty(E * G * N, dtype=torch.int32, device=dev)
+        L.check(lib.moeq_prep_scales(L.ptr(self.scales), L.ptr(self.zeros), E, G, N, dq_mode,
                                      L.ptr(self.sz), st), "moeq_prep_scales")
         self.sz_off = torch.tensor(_excl_cumsum([s.numel() for s in scales]), dtype=torch.int64, device=dev)
 

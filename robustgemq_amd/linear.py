@@ -134,8 +134,8 @@ class QuantLinear(nn.Module):
         M = x2.shape[0]
         if M == 0:
             return x.new_empty((*lead, self.out_features))
-        # LDS-staged tiles address rows with 32-bit offsets: run the rows in
-        # slices that each stay within 2 GiB
+        # the tiles address rows with 32-bit offsets: run the rows in slices
+        # that each stay within 2 GiB
         rows_max = max(16, (ops.A_ROWS_MAX_BYTES // (K * 2)) // 16 * 16)
         if M > rows_max:
             y = torch.cat([self._gemm(x2[r:r + rows_max]) for r in range(0, M, rows_max)])

@@ -85,15 +85,15 @@ def permute(idx, n_experts, n_shared=0, bm=16):
 
 
 # ------------------------------------------------------------- expert GEMMs
-# Row tiles of 32 rows and more stage A through LDS with 32-bit byte offsets:
-# every row they read must end within the first 2 GiB of `a`.
+# Every row tile reads A through buffer loads with 32-bit byte offsets:
+# every row it reads must end within the first 2 GiB of `a`.
 A_ROWS_MAX_BYTES = 1 << 31
 
 
 def a_rows_addressable(a, bm):
-    """True when every row of `a` can feed a tile of class bm: 16-row tiles
-    load rows with 64-bit addresses, larger ones need the rows within 2 GiB."""
-    return bm < 32 or a.shape[0] * a.stride(0) * a.element_size() <= A_ROWS_MAX_BYTES
+    """True when every row of `a` ends within the 2 GiB the tiles address
+    (any tile class bm)."""
+    return a.shape[0] * a.stride(0) * a.element_size() <= A_ROWS_MAX_BYTES
 
 
 def grouped_gemm(a, rows, n_out, tiles, n_tiles, max_tiles, bm, p0, p1=None, row_src=None,

@@ -74,7 +74,7 @@ def test_gpu_packing_matches_golden(device, nbits):
     w256, _ = ops.pack_weights_over_cols(codes[:, :256].contiguous(), nbits)
     s = torch.ones((256 // 64, 16), dtype=torch.float16, device=device)
     proj = QuantProjection([w256], [s], [torch.zeros_like(s)], [nbits], 256, 16, 64, 0)
-    np.testing.assert_array_equal(to_np(proj.words).view(np.uint32).reshape(2, 16, 4, nbits),
+    np.testing.assert_array_equal(to_np(proj.words).view(np.uint32).reshape(1, 2, 16, 4, nbits),
                                   GOLD[f"pack_b{nbits}_build"])
 
 

@@ -39,16 +39,30 @@ def test_pack_and_repack_bit_exact(device, nbits):
     s = (rng.standard_normal((G, N)) * 0.01).astype(np.float16)
     z = rng.integers(0, 1 << nbits, size=(G, N)).astype(np.float16)
     Kb = 512
+    Gb = Kb // 64
     codes_b = codes[:, :Kb]
     wb, _ = ops.pack_weights_over_cols(torch.from_numpy(codes_b).to(device), nbits)
-    for zz, want_mode in ((z, 2), (z + np.float16(0.25), 0)):  # integer zeros select the integer mode
-        proj = QuantProjection([wb], [torch.from_numpy(s[:Kb // 64]).to(device)],
-                               [torch.from_numpy(zz[:Kb // 64]).to(device)], [nbits], Kb, N, 64, 0)
+    # a second expert of other bits: each expert's block at its own offset
+    bits2 = nbits % 4 + 1
+    codes2 = rng.integers(0, 1 << bits2, size=(N, Kb)).astype(np.uint8)
+    w2, _ = ops.pack_weights_over_cols(torch.from_numpy(codes2).to(device), bits2)
+    s2 = (rng.standard_normal((Gb, N)) * 0.01).astype(np.float16)
+    z2 = rng.integers(0, 1 << bits2, size=(Gb, N)).astype(np.float16)
+    for zz, zz2, want_mode in ((z, z2, 2), (z + np.float16(0.25), z2, 0)):  # integer zeros: the integer mode
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+        proj = QuantProjection([wb, w2], [t(s[:Gb]), t(s2)], [t(zz[:Gb]), t(zz2)], [nbits, bits2], Kb, N, 64, 0)
         assert proj.dq_mode == want_mode
-        np.testing.assert_array_equal(to_np(proj.words).view(np.uint32).reshape(Kb // 128, N, 4, nbits),
+        words = to_np(proj.words).view(np.uint32)
+        n0 = N * Kb * nbits // 32
+        np.testing.assert_array_equal(words[:n0].reshape(N // 16, Kb // 128, 16, 4, nbits),
                                       oq.repack_build(codes_b, nbits))
-        np.testing.assert_array_equal(to_np(proj.sz).view(np.uint32),
-                                      oq.prep_scales(s[:Kb // 64], zz[:Kb // 64], want_mode))
+        np.testing.assert_array_equal(words[n0:].reshape(N // 16, Kb // 128, 16, 4, bits2),
+                                      oq.repack_build(codes2, bits2))
+        sz = to_np(proj.sz).view(np.uint32)
+        np.testing.assert_array_equal(sz[:Gb * N].reshape(N // 16, Gb, 16),
+                                      oq.prep_scales(s[:Gb], zz[:Gb], want_mode))
+        np.testing.assert_array_equal(sz[Gb * N:].reshape(N // 16, Gb, 16),
+                                      oq.prep_scales(s2, zz2, want_mode))
 
 
 # ------------------------------------------------------------------ routing

@@ -73,8 +73,12 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert rc == -1 and "nbits" in msg
     rc, msg = _err(lib.moeq_repack(fake, 100, 16, 2, fake, None))
     assert rc == -1 and "128" in msg
-    rc, msg = _err(lib.moeq_prep_scales(fake, fake, 10, 7, fake, None))
-    assert rc == -1
+    rc, msg = _err(lib.moeq_repack(fake, 128, 24, 2, fake, None))
+    assert rc == -1 and "16" in msg
+    rc, msg = _err(lib.moeq_prep_scales(fake, fake, 1, 2, 16, 7, fake, None))
+    assert rc == -1 and "dq_mode" in msg
+    rc, msg = _err(lib.moeq_prep_scales(fake, fake, 1, 2, 24, 0, fake, None))
+    assert rc == -1 and "multiple of 16" in msg
     # route: top_k > E, unsupported hidden size
     rc, msg = _err(lib.moeq_route(fake, L.F16, 4, 2048, fake, L.F16, None, 8, 9, 0, None, fake, fake, None, 0, None))
     assert rc == -1 and "top_k" in msg
@@ -128,10 +132,9 @@ def test_silu_mul_argument_checks():
 
 
 def test_activation_rows_2gib_guard():
-    """Row tiles of 32+ rows address activation rows with 32-bit offsets: the
-    operator refuses activations whose rows end past 2 GiB (16-row tiles use
-    64-bit addresses and take any), and QuantLinear slices its rows so every
-    slice fits."""
+    """Every row tile addresses activation rows with 32-bit offsets: the
+    operator refuses activations whose rows end past 2 GiB, whatever the tile
+    class, and QuantLinear slices its rows so every slice fits."""
     from types import SimpleNamespace
 
     from robustgemq_amd import ops
@@ -144,7 +147,8 @@ def test_activation_rows_2gib_guard():
     assert ops.a_rows_addressable(fake(fit, K), 128)
     assert not ops.a_rows_addressable(fake(fit + 1, K), 128)
     assert not ops.a_rows_addressable(fake(fit + 1, K), 32)
-    assert ops.a_rows_addressable(fake(4 * fit, K), 16)
+    assert not ops.a_rows_addressable(fake(fit + 1, K), 16)
+    assert ops.a_rows_addressable(fake(fit, K), 16)
     for K in (128, 2048, 4096, 14336, 1 << 20):
         rows_max = max(16, (ops.A_ROWS_MAX_BYTES // (K * 2)) // 16 * 16)  # QuantLinear's slice
         assert ops.a_rows_addressable(fake(rows_max, K), 128) or rows_max == 16

@@ -166,21 +166,40 @@ def test_build_layout_round_trip_and_bit_positions(nbits):
     N, K = 32, 256
     codes = rng.integers(0, 1 << nbits, size=(N, K)).astype(np.uint8)
     words = quant.repack_build(codes, nbits)
-    assert words.shape == (K // 128, N, 4, nbits)
+    assert words.shape == (N // 16, K // 128, 16, 4, nbits)
     np.testing.assert_array_equal(quant.unpack_build(words, nbits, N, K), codes)
-    # single code: k = 128 c + 32 kb + 8 t + 2 d + h lands in half h of one word
-    for k in (0, 1, 9, 37, 127, 200):
+    # single code: k = 128 c + 32 kb + 8 t + 2 d + h of column n lands in half h
+    # of one word of panel n // 16, row n % 16
+    for n, k in ((5, 0), (5, 1), (21, 9), (5, 37), (30, 127), (16, 200)):
         one = np.zeros((N, K), np.uint8)
-        one[5, k] = 1
+        one[n, k] = 1
         w = quant.repack_build(one, nbits)
         c, kb, i = k // 128, (k % 128) // 32, k % 32
         t, d, h = i // 8, (i % 8) // 2, i % 2
         nz = np.argwhere(w)
-        assert len(nz) == 1 and tuple(nz[0][:3]) == (c, 5, kb)
+        assert len(nz) == 1 and tuple(nz[0][:4]) == (n // 16, c, n % 16, kb)
+        # flat word index as the kernels address it
+        flat = np.flatnonzero(w.reshape(-1))[0]
+        assert flat // nbits == ((n // 16 * (K // 128) + c) * 64 + (n % 16) * 4 + kb)
         bit = int(np.log2(int(w[tuple(nz[0])])))
         assert (bit >= 16) == bool(h)
         pos = {4: 4 * d, 2: 2 * (4 * (t % 2) + d), 1: 4 * t + d, 3: 2 * (4 * (t % 2) + d)}[nbits]
         assert bit - 16 * h == pos
+
+
+def test_prep_scales_panel_order_and_values():
+    """Pair (g, n) lands at dword (n // 16 * G + g) * 16 + n % 16, holding
+    fp16 s in the low half and the mode's zero term in the high half."""
+    rng = np.random.default_rng(3)
+    G, N = 6, 48
+    s = (rng.standard_normal((G, N)) * 0.01).astype(np.float16)
+    z = rng.integers(0, 16, size=(G, N)).astype(np.float16)
+    for mode, zterm in ((0, -z), (1, z), (2, -(1024.0 + z.astype(np.float64)))):
+        flat = quant.prep_scales(s, z, mode).reshape(-1)
+        for g, n in ((0, 0), (5, 47), (2, 17), (3, 31), (1, 16)):
+            v = int(flat[(n // 16 * G + g) * 16 + n % 16])
+            assert np.uint16(v & 0xFFFF) == s[g, n].view(np.uint16)
+            assert np.uint16(v >> 16) == np.float16(zterm[g, n]).view(np.uint16)
 
 
 # ----------------------------------------------------------------- routing
