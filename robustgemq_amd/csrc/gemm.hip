@@ -58,7 +58,6 @@ int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq
   g.N = p0->N;
   g.group_size = p0->group_size;
   g.gshift = (p0->group_size & (p0->group_size - 1)) ? -1 : __builtin_ctz(unsigned(p0->group_size));
-  g.gmagic = uint32_t(((uint64_t(1) << 32) + uint64_t(p0->group_size) - 1) / uint64_t(p0->group_size));
   g.dq_mode = p0->dq_mode;
   g.p[0] = ProjDev{p0->words, p0->word_off, p0->sz, p0->sz_off, p0->nbits};
   g.p[1] = p1 ? ProjDev{p1->words, p1->word_off, p1->sz, p1->sz_off, p1->nbits} : g.p[0];

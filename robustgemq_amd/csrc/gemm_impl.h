@@ -45,9 +45,6 @@ struct GemmArgs {
   const int32_t *tiles;
   const int32_t *n_tiles;
   int K, N, group_size, gshift, dq_mode;  // gshift = log2(group_size), or -1
-  // group index of reduction index k: umulhi(k, gmagic) = k / group_size
-  // (gmagic = ceil(2^32 / group_size), exact for k * group_size < 2^32)
-  uint32_t gmagic;
   ProjDev p[2];
   void *out;
   int64_t ldo, split_stride;
@@ -417,21 +414,32 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
       const int cn = min(c + 1, c1 - 1);
       load_a(cn, Awr);
       load_b(cn, wnxt, snxt);
+      // A fragments in (step, row block) order, each read from LDS one row
+      // block ahead: the scheduling groups pin every read before the MFMAs of
+      // the previous fragment, so its latency runs under them (left to
+      // itself the scheduler reads two fragments and waits for them at once)
+      f16x8 Acur = __builtin_bit_cast(f16x8, Ard[l16][(4 * kb) ^ l16]);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         f16x8 B[NP][NB];
+        if (t == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) B[p][nb] = deq_frag<BITS, DQ>(wcur[p][nb], scur[p][nb], t);
 #pragma unroll
         for (int mb = 0; mb < MBA; ++mb) {
-          const f16x8 A = __builtin_bit_cast(f16x8, Ard[mb * 16 + l16][(4 * kb + t) ^ l16]);
+          f16x8 Anext = Acur;
+          if (mb + 1 < MBA) Anext = __builtin_bit_cast(f16x8, Ard[(mb + 1) * 16 + l16][(4 * kb + t) ^ l16]);
+          else if (t < 3) Anext = __builtin_bit_cast(f16x8, Ard[l16][(4 * kb + t + 1) ^ l16]);
 #pragma unroll
           for (int p = 0; p < NP; ++p)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-              acc[p][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[p][nb], acc[p][mb][nb], 0, 0, 0);
+              acc[p][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Acur, B[p][nb], acc[p][mb][nb], 0, 0, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, NP * NB, 0);  // MFMA
+          Acur = Anext;
         }
       }
       advance();
