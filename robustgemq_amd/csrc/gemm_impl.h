@@ -567,18 +567,19 @@ __device__ __forceinline__ void gemm_tile_mba(const GemmArgs &g, int e, int row0
 // Block b of a launch of V live blocks -> block L of the tile list (tile
 // L / n_ntiles, column tile L % n_ntiles).  Work-groups are dealt to the 8
 // XCDs round-robin, so XCD x = b % 8 takes its k-th block as block L: the
-// list (first V8 = V & ~7 blocks) is cut into 8 * XG segments of ln blocks,
-// ln one row tile's column tiles (at most an eighth of an XCD's share), and
-// XCD x gets segments x, x + 8, x + 16, ... (XG of them).  The schedule lists
-// the largest tiles first, so every XCD starts its longest tiles first and
-// gets an even share of each tile size, while a segment keeps a row tile's
-// column tiles (which read the same activation rows) on one L2; the
-// per % XG blocks left over go to the XCDs as equal runs after the segments.
+// list (first V8 = V & ~7 blocks) is cut into 64 segments of ln = V8 / 64
+// blocks and XCD x gets segments x, x + 8, x + 16, ...  A segment keeps
+// neighbouring tiles together (a row tile's column tiles, then the expert's
+// next row tile), so they share the expert's weights and the activation rows
+// through one L2, while tiles of different sizes (the list runs largest
+// first) spread over the XCDs; the blocks left over go to the XCDs as equal
+// runs after the segments.
 __device__ __forceinline__ unsigned xcd_block(unsigned b, unsigned V, unsigned n_ntiles) {
   const unsigned V8 = V & ~7u;
   if (b >= V8) return b;
-  const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3;
-  const unsigned ln = max(1u, min(n_ntiles, per / 8u)), XG = per / ln;
+  constexpr unsigned XG = 8;
+  const unsigned x = b & 7u, k = b >> 3, per = V8 >> 3, ln = per / XG;
+  if (ln == 0) return x * per + k;
   return k < XG * ln ? ((k / ln) * 8u + x) * ln + k % ln : 8u * XG * ln + x * (per - XG * ln) + (k - XG * ln);
 }
 

@@ -135,23 +135,23 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
   const int B = (m + 15) / 16;
   const int nt = (B + smax - 1) / smax;
   const int x = smax == s2 ? nt : min(nt, max(0, (B - s2 * nt + (smax - s2) - 1) / (smax - s2)));
-  // The list runs by kernel variant, largest first: class 0 = tiles of more
-  // than s2 blocks (the largest variant), class 1 = more than the variant
-  // below s2, class 2 = the rest; experts in order within a class.  An
-  // expert's classes never decrease along its tiles, so its tiles keep their
-  // order; the dispatcher starts the longest tiles first and the short ones
-  // fill the end of the launch.
+  // The list runs by kernel variant of each expert's first (largest) tile,
+  // largest first: class 0 = more than s2 blocks (the largest variant),
+  // class 1 = more than the variant below s2, class 2 = the rest; experts in
+  // order within a class, and an expert's tiles together, so they run at the
+  // same time and share the expert's weights through one L2 (listed by
+  // their own classes, an expert's second tile ran a round later and fetched
+  // the weights again).  The dispatcher starts the longest tiles first and
+  // the short ones fill the end of the launch.
   const int below = tile_blocks_below2(bm);
   auto tile_blocks = [&](int j, int &b0) {
     b0 = j < x ? j * smax : x * smax + (j - x) * s2;
     return min(b0 + (j < x ? smax : s2), B) - b0;
   };
   auto cls = [&](int nb) { return nb > s2 ? 0 : nb > below ? 1 : 2; };
-  uint64_t mine = 0;
-  for (int j = 0; j < nt; ++j) {
-    int b0;
-    mine += uint64_t(1) << (21 * cls(tile_blocks(j, b0)));
-  }
+  int b00;
+  const int ecls = nt > 0 ? cls(tile_blocks(0, b00)) : 0;
+  const uint64_t mine = uint64_t(nt) << (21 * ecls);
   __shared__ uint64_t sh64[17];
   int tot_rows;
   uint64_t tot_cls;
@@ -176,8 +176,7 @@ __device__ int schedule(int c, int E, int n_shared, int64_t T, int bm, int max_t
     // last one holds at least one block
     int b0;
     const int nb = tile_blocks(j, b0);
-    const int k = cls(nb);
-    const int at = k == 0 ? pos0++ : k == 1 ? pos1++ : pos2++;
+    const int at = ecls == 0 ? pos0++ : ecls == 1 ? pos1++ : pos2++;
     if (at >= max_tiles) continue;
     const int r0 = 16 * b0, r1 = min(16 * (b0 + nb), m);
     int32_t *tp = tiles + 4 * at;

@@ -131,13 +131,18 @@ def _check_routing_in_workspace(L, T, x32, lg):
     want = [(e, int(ref_perm["offsets"][e]) + r0, rc, 0)
             for e in range(E + S) for r0, rc in (split_rows(int(ref_perm["counts"][e]), plan["bm"])
                                                   if ref_perm["counts"][e] else [])]
-    # listed by the kernel variant a tile runs, largest first: more than s2
-    # 16-row blocks, then more than the variant below s2, then the rest;
-    # experts in order within each group (a stable sort)
+    # listed by the kernel variant of each expert's first (largest) tile,
+    # largest first: more than s2 16-row blocks, then more than the variant
+    # below s2, then the rest; experts in order within each group and an
+    # expert's tiles together (a stable sort on the expert's key)
     s2 = {16: 1, 32: 2, 64: 4, 128: 8, 256: 10}[plan["bm"]]
     below = {64: 2, 128: 4, 256: 8}.get(plan["bm"], 0)
     blocks = lambda rc: -(-rc // 16)
-    want.sort(key=lambda t: 0 if blocks(t[2]) > s2 else 1 if blocks(t[2]) > below else 2)
+    cls = lambda rc: 0 if blocks(rc) > s2 else 1 if blocks(rc) > below else 2
+    first = {}
+    for t in want:
+        first.setdefault(t[0], cls(t[2]))
+    want.sort(key=lambda t: first[t[0]])
     np.testing.assert_array_equal(tiles, np.array(want, np.int32).reshape(-1, 4))
     return ref_idx, ref_w
 
