@@ -250,7 +250,9 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   if (ev0 && (rc = hip_ok(hipEventRecord(ev0, as_stream(stream)), "moe: event record"))) return rc;
   // a token picks an expert at most once: no tile holds more than T rows
   const int max_rows = int(std::min<int64_t>(T, tile_rows(p.bm)));
-  rc = grouped_gemm_rows(&gu, &m->w1, &m->w3, max_rows, stream);
+  // average rows per routed expert if the pairs spread over as many experts as they can
+  const int rows_hint = int(T * m->top_k / std::max<int64_t>(1, std::min<int64_t>(m->n_experts, T * m->top_k)));
+  rc = grouped_gemm_rows(&gu, &m->w1, &m->w3, max_rows, rows_hint, stream);
   if (rc) return rc;
   if (ev1 && (rc = hip_ok(hipEventRecord(ev1, as_stream(stream)), "moe: event record"))) return rc;
 
@@ -270,7 +272,7 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   dn.ldo = m->hidden;
   dn.splits = p.splits;
   dn.split_stride = p.rows * m->hidden;
-  rc = grouped_gemm_rows(&dn, &m->w2, nullptr, max_rows, stream);
+  rc = grouped_gemm_rows(&dn, &m->w2, nullptr, max_rows, rows_hint, stream);
   if (rc) return rc;
 
   return moeq_combine(at(p.off_y), p.y_dtype, p.splits, p.rows * m->hidden, m->hidden, inv, w, T,

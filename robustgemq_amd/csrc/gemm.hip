@@ -22,7 +22,7 @@ static int check_proj(const moeq_proj *p, const char *name) {
   return MOEQ_OK;
 }
 
-int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows,
+int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, int rows_hint,
                             void *stream) {
   if (!gm) return fail(MOEQ_ERR_INVALID, "grouped_gemm: null descriptor");
   if (!gm->a || !gm->tiles || !gm->n_tiles || !gm->out) return fail(MOEQ_ERR_INVALID, "grouped_gemm: null pointer");
@@ -67,6 +67,7 @@ int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq
   g.nchunks = nchunks;
   g.chunks_per_split = int(cdiv(nchunks, gm->splits));
   g.max_rows = max_rows;
+  g.rows_hint = rows_hint;
   hipStream_t s = as_stream(stream);
   const int mt = gm->max_tiles, sp = gm->splits;
   const bool silu = gm->epilogue == MOEQ_EPI_SILU_MUL;
@@ -82,7 +83,7 @@ int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq
 
 extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
                                  const moeq_proj *p1, void *stream) {
-  return grouped_gemm_rows(gm, p0, p1, 0, stream);
+  return grouped_gemm_rows(gm, p0, p1, 0, 0, stream);
 }
 
 // Column tile width the kernels use for a given (bm, epilogue); the layer

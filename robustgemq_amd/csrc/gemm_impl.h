@@ -52,6 +52,9 @@ struct GemmArgs {
   // most rows any tile of this launch can hold (0: the class capacity);
   // 16-row launches at most 16 run the kernel without the two-block path
   int max_rows;
+  // average rows per hit expert the caller expects (0: unknown); 16-row
+  // launches of tall tiles take twice the columns per wave
+  int rows_hint;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -350,7 +353,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int e, int row0, in
     // KS: partial sums of the NW waves -> wave 0, added in wave order
     if constexpr (KS) {
       float *red = reinterpret_cast<float *>(&As0[0][0]);
-      static_assert((NW - 1) * NP * MBA * NB * 4 * 64 * 4 <= 48 * 16 * 16, "K-split partials exceed As0");
+      static_assert((NW - 1) * NP * MBA * NB * 4 * 64 * 4 <= 96 * 16 * 16, "K-split partials exceed As0");
       if (wave > 0) {
 #pragma unroll
         for (int p = 0; p < NP; ++p)
@@ -597,10 +600,10 @@ __global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel
   const int mt = int(L / unsigned(g.n_ntiles));
   const int nt = int(L % unsigned(g.n_ntiles));
   // 16-row blocks use As0 for the cross-wave reduction: (NW - 1) * NP * MBA *
-  // NB * 4 floats per lane, at most 12 KB.  The prefill classes hold tile_rows(BM)
+  // NB * 4 floats per lane, at most 24 KB.  The prefill classes hold tile_rows(BM)
   // rows per buffer (two 40 KB buffers for the 160-row class: two
   // work-groups fill the 160 KB of LDS).
-  __shared__ uint4 As0[BM == 16 ? 48 : tile_rows(BM)][16];
+  __shared__ uint4 As0[BM == 16 ? 96 : tile_rows(BM)][16];
   __shared__ uint4 As1[BM == 16 ? 1 : tile_rows(BM)][16];
   const int32_t *tp = g.tiles + 4 * mt;
   const int e = tp[0], row0 = tp[1], mcount = tp[2];
@@ -646,7 +649,8 @@ template <> struct Shape<256, false> { static constexpr int NW = 4, NB = 4; };
 // moeq_grouped_gemm for callers that know the most rows any tile holds
 // (max_rows > 0; the layer forward: at most T per expert), which lets 16-row
 // launches of at most 16 rows per tile skip the two-block kernel path.
-int grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, void *stream);
+int grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, int rows_hint,
+                      void *stream);
 
 // One-token forwards: the down projection of the k routed rows plus the
 // shared rows and the weighted combine in one launch (decode1.hip), given
@@ -659,16 +663,16 @@ template <int BM>
 int launch_grouped_gemm(const GemmArgs &g, bool silu, int a_dtype, int out_dtype, int max_tiles, int splits,
                         hipStream_t s);
 
-template <int BM, bool SILU, int ADT, int ODT, bool KS = false, bool MB2 = true>
+template <int BM, bool SILU, int ADT, int ODT, bool KS = false, bool MB2 = true, int NBW = Shape<BM, SILU>::NB>
 inline int launch_one(const GemmArgs &g0, int max_tiles, int splits, hipStream_t s) {
   using S = Shape<BM, SILU>;
   static_assert(!KS || BM == 16, "K split over waves is a 16-row block variant");
   GemmArgs g = g0;
-  g.n_ntiles = int(cdiv(g.N, tile_cols<S, KS>()));
+  g.n_ntiles = int(cdiv(g.N, KS ? NBW * 16 : S::NW * NBW * 16));
   const int64_t blocks = int64_t(max_tiles) * g.n_ntiles;
   if (blocks > 0x7fffffff) return fail(MOEQ_ERR_UNSUPPORTED, "grouped_gemm: grid too large");
   dim3 grid(unsigned(blocks), 1, unsigned(splits)), block(S::NW * 64);
-  grouped_gemm_kernel<BM, S::NW, S::NB, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ADT, ODT, KS, MB2>
+  grouped_gemm_kernel<BM, S::NW, NBW, SILU ? 2 : 1, SILU ? MOEQ_EPI_SILU_MUL : MOEQ_EPI_STORE, ADT, ODT, KS, MB2>
       <<<grid, block, 0, s>>>(g);
   return check_launch("grouped_gemm");
 }
