@@ -11,6 +11,12 @@ extern "C" int moeq_gemm_tile_n(int bm, int epilogue);
 
 namespace moeq {
 
+// One-token layers whose gate matrix is at least this large route in two
+// launches (logits over the whole GPU, then a one-wave top-k).  Measured per
+// layer: Qwen3-shaped (512 KB) 32.7 -> 28.5 us; OLMoE-shaped (256 KB) 26.0 ->
+// 27.0 and Mixtral-shaped (64 KB) 61.2 -> 67.9 us, so those keep route1.
+constexpr int64_t kSplitRoute1Bytes = 512 * 1024;
+
 static thread_local char g_err[512] = "";
 
 int fail(int code, const char *fmt, ...) {
@@ -186,7 +192,13 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
     // Mixtral's one-token router ranks and renormalises 16-bit probabilities
     const bool act_softmax = T == 1 && m->one_token_act_softmax;
     if (act_softmax) r1.prob_dtype = m->act_dtype;
-    if (launch_route1(r1, po, s)) {
+    // A large gate matrix is read faster by one logit per wave over the whole
+    // GPU and a one-wave top-k after it than by route1's single work-group.
+    const int64_t gate_bytes = int64_t(m->n_experts) * m->hidden * (m->gate_dtype == MOEQ_F32 ? 4 : 2);
+    if (T == 1 && gate_bytes >= kSplitRoute1Bytes && m->n_experts <= 256 && m->top_k <= kMaxTopK) {
+      if ((rc = launch_route_logits(ra, s))) return rc;
+      if ((rc = launch_topk1(lg, lg_dt, r1, po, s))) return rc;
+    } else if (launch_route1(r1, po, s)) {
       if ((rc = check_launch("moe/route1"))) return rc;
     } else if (act_softmax) {
       return fail(MOEQ_ERR_UNSUPPORTED, "moe: one_token_act_softmax needs the one-token router "

@@ -280,6 +280,61 @@ static void launch_logits_topk_dt(const RouteArgs &a, int maxch, hipStream_t s) 
 }
 
 // ---------------------------------------------------------------- one token
+// One token's top-k and grouping from its E rounded logits (one wave): ranks
+// them (topk_ranks), writes idx / w and the permutation, which for one token
+// is the selected experts in id order, one 1-row tile each, then the shared
+// experts' rows (moeq_permute's output for T = 1).
+__device__ __forceinline__ void one_token_grouping(const float *lg, const RouteArgs &a, const PermOut &po) {
+  const int lane = lane_id();
+  const int E = a.E, k = a.k;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  auto finish = [&](auto regs) {
+    constexpr int R = decltype(regs)::value;
+    float vals[R];
+    int rank[R];
+    float wsel[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) vals[r] = 64 * r + lane < E ? lg[64 * r + lane] : -INFINITY;
+    topk_ranks<R>(vals, E, k, a.norm, rank, wsel, a.prob_dtype);
+    int before = 0;  // selected experts in earlier registers
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int e = 64 * r + lane;
+      const bool sel = e < E && rank[r] < k;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(sel);
+      const int pos = before + __popcll(m & lt);  // row = selected experts below e
+      if (e < E) {
+        po.counts[e] = sel ? 1 : 0;
+        po.offsets[e] = pos;
+      }
+      if (sel) {
+        a.idx[rank[r]] = e;
+        a.w[rank[r]] = wsel[r];
+        po.row_pair[pos] = rank[r];
+        po.row_token[pos] = 0;
+        po.inv_perm[rank[r]] = pos;
+        *reinterpret_cast<int4 *>(po.tiles + 4 * pos) = (int4){e, pos, 1, 0};
+      }
+      before += __popcll(m);
+    }
+  };
+  const int ereg = ereg_for(E);
+  if (ereg == 1) finish(std::integral_constant<int, 1>{});
+  else if (ereg == 2) finish(std::integral_constant<int, 2>{});
+  else finish(std::integral_constant<int, 4>{});
+  // shared experts: one row each after the k routed rows
+  for (int v = lane; v < po.n_shared; v += 64) {
+    po.counts[E + v] = 1;
+    po.offsets[E + v] = k + v;
+    po.row_token[k + v] = 0;
+    *reinterpret_cast<int4 *>(po.tiles + 4 * (k + v)) = (int4){E + v, k + v, 1, 0};
+  }
+  if (lane == 0) {
+    po.offsets[E + po.n_shared] = k + po.n_shared;
+    *po.n_tiles = min(k + po.n_shared, po.max_tiles);
+  }
+}
+
 // Eight waves; wave w computes the logits of experts w * EE .. w * EE + EE - 1,
 // then (w + 8) * EE .., with every k step of the x row and of its EE gate
 // rows loaded at once (one memory round trip per expert group).  Each logit
@@ -358,53 +413,7 @@ __global__ __launch_bounds__(kR1Waves * 64) void route1_kernel(RouteArgs a, Perm
   }
   __syncthreads();
   if (wave != 0) return;
-  const int E = a.E, k = a.k;
-  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  auto finish = [&](auto regs) {
-    constexpr int R = decltype(regs)::value;
-    float vals[R];
-    int rank[R];
-    float wsel[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) vals[r] = 64 * r + lane < E ? lg[64 * r + lane] : -INFINITY;
-    topk_ranks<R>(vals, E, k, a.norm, rank, wsel, a.prob_dtype);
-    int before = 0;  // selected experts in earlier registers
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int e = 64 * r + lane;
-      const bool sel = e < E && rank[r] < k;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(sel);
-      const int pos = before + __popcll(m & lt);  // row = selected experts below e
-      if (e < E) {
-        po.counts[e] = sel ? 1 : 0;
-        po.offsets[e] = pos;
-      }
-      if (sel) {
-        a.idx[rank[r]] = e;
-        a.w[rank[r]] = wsel[r];
-        po.row_pair[pos] = rank[r];
-        po.row_token[pos] = 0;
-        po.inv_perm[rank[r]] = pos;
-        *reinterpret_cast<int4 *>(po.tiles + 4 * pos) = (int4){e, pos, 1, 0};
-      }
-      before += __popcll(m);
-    }
-  };
-  const int ereg = ereg_for(E);
-  if (ereg == 1) finish(std::integral_constant<int, 1>{});
-  else if (ereg == 2) finish(std::integral_constant<int, 2>{});
-  else finish(std::integral_constant<int, 4>{});
-  // shared experts: one row each after the k routed rows
-  for (int v = lane; v < po.n_shared; v += 64) {
-    po.counts[E + v] = 1;
-    po.offsets[E + v] = k + v;
-    po.row_token[k + v] = 0;
-    *reinterpret_cast<int4 *>(po.tiles + 4 * (k + v)) = (int4){E + v, k + v, 1, 0};
-  }
-  if (lane == 0) {
-    po.offsets[E + po.n_shared] = k + po.n_shared;
-    *po.n_tiles = min(k + po.n_shared, po.max_tiles);
-  }
+  one_token_grouping(lg, a, po);
 }
 
 // Expert group per wave: no larger than the experts need over 8 waves, and
@@ -441,6 +450,24 @@ bool launch_route1(const RouteArgs &a, const PermOut &po, hipStream_t s) {
   else if (x == MOEQ_BF16 && w == MOEQ_F32) launch_route1_dt<MOEQ_BF16, MOEQ_F32>(a, po, s);
   else return false;
   return true;
+}
+
+// One token from logits already computed (logits_kernel, one logit per
+// wave over the whole GPU): one wave reads the E rounded logits (stored in
+// `dtype`, exact since they were rounded to it) and writes what route1_kernel
+// writes.  For large gate matrices this beats route1_kernel, whose single
+// work-group reads the whole matrix.
+__global__ __launch_bounds__(64) void topk1_kernel(const void *logits, int dtype, RouteArgs a, PermOut po) {
+  __shared__ float lg[256];
+  for (int e = lane_id(); e < a.E; e += 64) lg[e] = load_as_f32(logits, dtype, e);
+  __syncthreads();
+  one_token_grouping(lg, a, po);
+}
+
+int launch_topk1(const void *logits, int dtype, const RouteArgs &a, const PermOut &po, hipStream_t s) {
+  if (a.E > 256 || a.k > kMaxTopK) return fail(MOEQ_ERR_UNSUPPORTED, "topk1: E=%d k=%d", a.E, a.k);
+  topk1_kernel<<<dim3(1), dim3(64), 0, s>>>(logits, dtype, a, po);
+  return check_launch("route/topk1");
 }
 
 // Fused logits + top-k for batches above T * E = 16384; returns false (and

@@ -316,4 +316,8 @@ struct PermOut {
 // launching otherwise (route.hip).
 bool launch_route1(const RouteArgs &a, const PermOut &po, hipStream_t s);
 
+// One token's top-k and grouping as route1_kernel writes them, from E logits
+// already in memory (`dtype`), in one wave (route.hip).
+int launch_topk1(const void *logits, int dtype, const RouteArgs &a, const PermOut &po, hipStream_t s);
+
 }  // namespace moeq

@@ -134,10 +134,12 @@ def test_layer_matches_oracle_deepseek_shared_zipf(device, T):
 
 @pytest.mark.parametrize("name", ["ref_test", "olmoe_mixed", "qwen3_mixed", "mixtral_small", "deepseek_v2_lite"])
 def test_one_token_forward_routing(device, name):
-    """A one-token forward routes and groups in a single launch; the logits it
-    returns and the selection, weights and permutation it leaves in its
-    workspace equal the oracle's (and moeq_route's weights) bit for bit, and
-    the output meets the layer bar."""
+    """A one-token forward routes and groups in a single launch (gate matrices
+    of 512 KB and more: a logits launch over the GPU and a one-wave top-k,
+    here qwen3_mixed and deepseek_v2_lite); the logits it returns and the
+    selection, weights and permutation it leaves in its workspace equal the
+    oracle's (and moeq_route's weights) bit for bit, and the output meets the
+    layer bar."""
     from robustgemq_amd import ops
     _say(f"[layer] one-token forward routing: {name}")
     cfg, w, block, dense = _layer(name)
