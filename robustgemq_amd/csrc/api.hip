@@ -264,7 +264,9 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   const int max_rows = int(std::min<int64_t>(T, tile_rows(p.bm)));
   // average rows per routed expert if the pairs spread over as many experts as they can
   const int rows_hint = int(T * m->top_k / std::max<int64_t>(1, std::min<int64_t>(m->n_experts, T * m->top_k)));
-  rc = grouped_gemm_rows(&gu, &m->w1, &m->w3, max_rows, rows_hint, stream);
+  // one token: each selected expert and each shared expert one 1-row tile
+  const int known_tiles = T == 1 ? m->top_k + m->n_shared : 0;
+  rc = grouped_gemm_rows(&gu, &m->w1, &m->w3, max_rows, rows_hint, known_tiles, stream);
   if (rc) return rc;
   if (ev1 && (rc = hip_ok(hipEventRecord(ev1, as_stream(stream)), "moe: event record"))) return rc;
 
@@ -284,7 +286,7 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
   dn.ldo = m->hidden;
   dn.splits = p.splits;
   dn.split_stride = p.rows * m->hidden;
-  rc = grouped_gemm_rows(&dn, &m->w2, nullptr, max_rows, rows_hint, stream);
+  rc = grouped_gemm_rows(&dn, &m->w2, nullptr, max_rows, rows_hint, known_tiles, stream);
   if (rc) return rc;
 
   return moeq_combine(at(p.off_y), p.y_dtype, p.splits, p.rows * m->hidden, m->hidden, inv, w, T,

@@ -23,7 +23,7 @@ static int check_proj(const moeq_proj *p, const char *name) {
 }
 
 int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, int rows_hint,
-                            void *stream) {
+                            int known_tiles, void *stream) {
   if (!gm) return fail(MOEQ_ERR_INVALID, "grouped_gemm: null descriptor");
   if (!gm->a || !gm->tiles || !gm->n_tiles || !gm->out) return fail(MOEQ_ERR_INVALID, "grouped_gemm: null pointer");
   int rc = check_proj(p0, "p0");
@@ -68,6 +68,7 @@ int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq
   g.chunks_per_split = int(cdiv(nchunks, gm->splits));
   g.max_rows = max_rows;
   g.rows_hint = rows_hint;
+  g.known_tiles = known_tiles > 0 && known_tiles <= gm->max_tiles ? known_tiles : 0;
   hipStream_t s = as_stream(stream);
   const int mt = gm->max_tiles, sp = gm->splits;
   const bool silu = gm->epilogue == MOEQ_EPI_SILU_MUL;
@@ -83,7 +84,7 @@ int moeq::grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq
 
 extern "C" int moeq_grouped_gemm(const moeq_gemm *gm, const moeq_proj *p0,
                                  const moeq_proj *p1, void *stream) {
-  return grouped_gemm_rows(gm, p0, p1, 0, 0, stream);
+  return grouped_gemm_rows(gm, p0, p1, 0, 0, 0, stream);
 }
 
 // Column tile width the kernels use for a given (bm, epilogue); the layer

@@ -55,6 +55,10 @@ struct GemmArgs {
   // average rows per hit expert the caller expects (0: unknown); 16-row
   // launches of tall tiles take twice the columns per wave
   int rows_hint;
+  // number of row tiles when the caller knows it (one-token forwards: k +
+  // shared experts), or 0: the launch then need not read it from n_tiles
+  // before its tile lookup
+  int known_tiles;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -593,7 +597,7 @@ __global__ __launch_bounds__(NW * 64, BM == 16 ? 1 : 2) void grouped_gemm_kernel
   // The grid is sized for the host-side bound on row tiles; blocks past the
   // real count (read from the device schedule) exit together; the live ones
   // are renumbered per XCD (xcd_block).
-  const unsigned V = unsigned(*g.n_tiles) * unsigned(g.n_ntiles);
+  const unsigned V = unsigned(g.known_tiles > 0 ? g.known_tiles : *g.n_tiles) * unsigned(g.n_ntiles);
   const unsigned b = blockIdx.x;
   if (b >= V) return;
   const unsigned L = xcd_block(b, V, unsigned(g.n_ntiles));
@@ -650,7 +654,7 @@ template <> struct Shape<256, false> { static constexpr int NW = 4, NB = 4; };
 // (max_rows > 0; the layer forward: at most T per expert), which lets 16-row
 // launches of at most 16 rows per tile skip the two-block kernel path.
 int grouped_gemm_rows(const moeq_gemm *gm, const moeq_proj *p0, const moeq_proj *p1, int max_rows, int rows_hint,
-                      void *stream);
+                      int known_tiles, void *stream);
 
 // One-token forwards: the down projection of the k routed rows plus the
 // shared rows and the weighted combine in one launch (decode1.hip), given
