@@ -71,14 +71,29 @@ __device__ __forceinline__ void load8(const void *p, int dtype, int64_t i, float
   }
 }
 
+// Maximum over the 64 lanes, returned in every lane (no NaN inputs): lane
+// pairs (xor 1, xor 2), the two quads of each half-row (half-row mirror), the
+// two halves of each row (row mirror), then row pairs and wave halves by
+// swapping them between two copies (v_permlane16/32_swap).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false)));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Top-k of the logits held by one wave (expert e = 64 r + lane in vals[r]),
 // ranked by value with ties to the lower index (NaN ranks last); softmax
 // weights over all E experts; optional renormalisation over the selected k.
 // topk_ranks leaves each expert's rank and routing weight in the lane that
-// holds it; select_topk writes row t.  Each expert's rank is counted
-// directly: every value is broadcast once (v_readlane) and compared with all
-// of them, so there is no sequential select-and-remove loop and no
-// dynamically indexed register.
+// holds it; select_topk writes row t.  The k selected experts are found by k
+// wave-wide argmax rounds (a DPP / permlane reduction each), so the cost
+// grows with k, not with E, and no register is indexed dynamically.  Every
+// round places one expert (k <= E), so all k slots of the row are written.
 //
 // prob_dtype F16 / BF16 restates a router that runs softmax on a 16-bit
 // tensor (F.softmax computes in fp32 and rounds its output), ranks those
@@ -111,22 +126,31 @@ __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&ra
 #pragma unroll
     for (int r = 0; r < EREG; ++r)
       vals[r] = 64 * r + lane < E ? round_logit(expf(vals[r] - mx) / den, prob_dtype) : -INFINITY;
+#pragma unroll
+    for (int r = 0; r < EREG; ++r)
+      if (vals[r] != vals[r]) vals[r] = -INFINITY;  // every logit -inf: NaN probabilities, rank last
   }
+  // k rounds of a wave-wide argmax over the experts not yet taken: round s
+  // takes the largest value, the lowest expert index among equal ones (the
+  // order of a stable descending sort), and gives it rank s; the others keep
+  // rank k.  +0 and -0 compare equal, as in the sort.
 #pragma unroll
-  for (int r = 0; r < EREG; ++r) rank[r] = 0;
-  float m = -INFINITY;
+  for (int r = 0; r < EREG; ++r) rank[r] = k;
+  float m = -INFINITY;  // the top value
+  for (int s = 0; s < k; ++s) {
+    float c = -INFINITY;
 #pragma unroll
-  for (int r2 = 0; r2 < EREG; ++r2) {
-    if (64 * r2 >= E) break;
-#pragma unroll 16
-    for (int l2 = 0; l2 < 64; ++l2) {
-      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vals[r2]), l2));
-      const int e2 = 64 * r2 + l2;
-      m = fmaxf(m, v);
+    for (int r = 0; r < EREG; ++r)
+      if (rank[r] == k && 64 * r + lane < E) c = fmaxf(c, vals[r]);
+    const float top = wave_max(c);
+    if (s == 0) m = top;
+    bool placed = false;
 #pragma unroll
-      for (int r = 0; r < EREG; ++r) {
-        const int e = 64 * r + lane;
-        rank[r] += (v > vals[r] || (v == vals[r] && e2 < e)) ? 1 : 0;
+    for (int r = 0; r < EREG; ++r) {
+      const uint64_t b = __builtin_amdgcn_ballot_w64(rank[r] == k && 64 * r + lane < E && vals[r] == top);
+      if (!placed && b != 0) {
+        placed = true;
+        if (lane == __builtin_ctzll(b)) rank[r] = s;
       }
     }
   }

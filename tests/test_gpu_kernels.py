@@ -93,6 +93,36 @@ def test_route_bit_exact(device, gate, T, H, E, k, norm):
     np.testing.assert_allclose(to_np(w2), ref_w, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 8), (96, 16), (300, 6)])
+def test_topk_special_values_and_ties(device, E, k):
+    """Selection order on hand-made logit rows: a stable descending sort
+    (equal values, +0 and -0 included, in index order), NaN ranked as -inf
+    (after every finite value; equal to -inf, so in index order), +inf first.  Rows mix these with coarse values (many
+    exact ties) and fine ones; E = 96 and 300 leave part of the last lane
+    register empty."""
+    from robustgemq_amd import ops
+    _say(f"[topk] special values E={E} k={k}")
+    rng = np.random.default_rng(E * 31 + k)
+    T = 64
+    lg = rng.integers(-3, 4, size=(T, E)).astype(np.float32) * 0.5  # many ties
+    lg[1::4] = rng.standard_normal((len(range(1, T, 4)), E)).astype(np.float32)
+    lg[2, :] = 0.0
+    lg[2, ::3] = -0.0
+    lg[3, :] = -np.inf
+    for t in range(4, T, 5):  # NaN / -inf holes, at least k finite values left
+        holes = rng.choice(E, size=E - k, replace=False)
+        lg[t, holes[: len(holes) // 2]] = np.nan
+        lg[t, holes[len(holes) // 2:]] = -np.inf
+    lg[5, rng.choice(E, size=min(k, 2), replace=False)] = np.inf
+    with np.errstate(invalid="ignore"):  # rows 3 and 5: non-finite weights, not compared
+        ref_idx, ref_w = orr.topk_route(np.where(np.isnan(lg), -np.inf, lg), k, True)
+    idx, w = ops.route_from_logits(torch.from_numpy(lg).to(device), k, True)
+    np.testing.assert_array_equal(to_np(idx), ref_idx)
+    finite = np.isfinite(ref_w).all(axis=1)
+    np.testing.assert_allclose(to_np(w)[finite], ref_w[finite], rtol=2e-6, atol=1e-7)
+    assert (to_np(idx)[3] == np.arange(k)).all()  # all -inf: index order
+
+
 def test_route_bias_and_ties(device):
     from robustgemq_amd import ops
     _say("[route] bias + ties")
