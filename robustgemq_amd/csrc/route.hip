@@ -130,42 +130,80 @@ __device__ __forceinline__ float halving_sum(float (&c)[64]) {
   return a[0];
 }
 
+// Copies kTT activation rows (16-bit, from token t0 on) to LDS as units
+// (tt, i, l) = the 8 values lane l multiplies at k step i: one 1 KB unit row
+// per wave instruction (buffer_load ... lds), then waits for every wave's
+// copies.  Rows past T and k steps past H copy a valid row, never read.
+// (A device function: with this builtin or the inline wait directly in the
+// kernel template's body, hipcc's host pass emitted no launch stub for it.)
+template <int MAXCH, int kTT, int NWV>
+__device__ __forceinline__ void stage_rows(uint4 *xs, __amdgpu_buffer_rsrc_t xrs, const RouteArgs &a, int64_t t0,
+                                           int wave, int lane) {
+  for (int q = wave; q < kTT * MAXCH; q += NWV) {
+    const int tt = q / MAXCH, i = q % MAXCH;
+    const uint32_t kc = uint32_t(min(512 * i + 8 * lane, a.H - 8));
+    const uint32_t row = uint32_t(min(int64_t(tt), a.T - 1 - t0)) * uint32_t(a.H) * 2u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *)&xs[q * 64], 16, kc * 2u,
+                                             row, 0, 0);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 template <int XDT, int WDT, int NWV, int MAXCH, int kTT>
 __global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
   // kTT tokens x kEE experts per wave pass (64 chains per lane); the chain
   // order and the lane reduction do not depend on the split
   constexpr int kEE = 64 / kTT;
   __shared__ float lg[kTT][512];
+  // 16-bit activations: the block's kTT rows are copied to LDS once, as
+  // units (tt, i, l) = the 8 values lane l multiplies at k step i, so the k
+  // loop waits only for gate rows (from L2), fetched one step ahead
+  constexpr bool XL = XDT != MOEQ_F32;
+  __shared__ uint4 xs[XL ? kTT * MAXCH * 64 : 1];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t0 = int64_t(blockIdx.x) * kTT;
   const int n_eb = (a.E + kEE - 1) / kEE;
-  // two k steps in flight for fp16 rows; widened operands need the registers
-  constexpr int NBUF = (XDT == MOEQ_F16 && WDT == MOEQ_F16) ? 2 : 1;
+  // Rows are read through buffer resources based at this block's first token
+  // / expert: one 32-bit lane offset (the k position) serves all rows, whose
+  // row offsets are uniform.  Rows past T or E, and k steps past H, load a
+  // valid row (token T - 1, expert E - 1, k = H - 8) that is never used, so
+  // the loads are unconditional.
+  constexpr uint32_t XES = XDT == MOEQ_F32 ? 4 : 2, WES = WDT == MOEQ_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(static_cast<const char *>(a.x) + t0 * a.H * XES), (short)0, 0x7fffffff, 0x00020000);
+  auto kcol = [&](int i) { return uint32_t(min(512 * i + 8 * lane, a.H - 8)); };
+  auto xrow = [&](int tt) { return uint32_t(min(int64_t(tt), a.T - 1 - t0)) * uint32_t(a.H) * XES; };
+  if constexpr (XL) stage_rows<MAXCH, kTT, NWV>(xs, xrs, a, t0, wave, lane);
+  const uint4 *const xsp = xs;
+  // gate rows of fp16 / bf16 gates two k steps in flight; fp32 gate rows
+  // (twice the registers) and fp32 activations one
+  constexpr int NBUF = (XL && WDT != MOEQ_F32) ? 2 : 1;
   for (int eb = wave; eb < n_eb; eb += NWV) {
     const int e0 = eb * kEE;
     float ch[kTT * kEE];
 #pragma unroll
     for (int i = 0; i < kTT * kEE; ++i) ch[i] = 0.f;
-    // Rows are read through buffer resources based at this block's first
-    // token / expert: one 32-bit lane offset (the k position) serves all 16
-    // rows, whose row offsets are uniform.  Rows past T or E, and k steps past
-    // H, load a valid row (token T - 1, expert E - 1, k = H - 8) that is never
-    // used, so the loads are unconditional.
-    constexpr uint32_t XES = XDT == MOEQ_F32 ? 4 : 2, WES = WDT == MOEQ_F32 ? 4 : 2;
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char *>(static_cast<const char *>(a.x) + t0 * a.H * XES), (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char *>(static_cast<const char *>(a.wg) + int64_t(e0) * a.H * WES), (short)0, 0x7fffffff,
         0x00020000);
-    auto fetch = [&](int i, Raw8<XDT> (&xb)[kTT], Raw8<WDT> (&wb)[kEE]) {
-      const uint32_t kc = uint32_t(min(512 * i + 8 * lane, a.H - 8));
-#pragma unroll
-      for (int tt = 0; tt < kTT; ++tt)
-        xb[tt].load(xrs, kc * XES, uint32_t(min(int64_t(tt), a.T - 1 - t0)) * uint32_t(a.H) * XES);
+    auto fetch_w = [&](int i, Raw8<WDT> (&wb)[kEE]) {
+      const uint32_t kc = kcol(i);
 #pragma unroll
       for (int ee = 0; ee < kEE; ++ee)
         wb[ee].load(wrs, kc * WES, uint32_t(min(ee, a.E - 1 - e0)) * uint32_t(a.H) * WES);
+    };
+    auto fetch_x = [&](int i, Raw8<XDT> (&xb)[kTT]) {
+#pragma unroll
+      for (int tt = 0; tt < kTT; ++tt) {
+        if constexpr (XL) {
+          const uint4 v = xsp[(tt * MAXCH + i) * 64 + lane];
+          xb[tt].u[0] = v.x; xb[tt].u[1] = v.y; xb[tt].u[2] = v.z; xb[tt].u[3] = v.w;
+        } else {
+          xb[tt].load(xrs, kcol(i) * XES, xrow(tt));
+        }
+      }
     };
     auto step = [&](int i, const Raw8<XDT> (&xb)[kTT], const Raw8<WDT> (&wb)[kEE]) {
       const int k0 = 512 * i + 8 * lane;
@@ -198,20 +236,27 @@ __global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
       }
     };
     if constexpr (NBUF == 2) {
-      // k steps i (rows A) and i + 1 (rows B) per trip: the next step's rows
-      // are in flight while one step is multiplied
-      Raw8<XDT> xa[kTT], xb[kTT];
+      // k steps i (gate rows A) and i + 1 (rows B) per trip: the next step's
+      // rows are in flight while one step is multiplied
       Raw8<WDT> wa[kEE], wb[kEE];
-      fetch(0, xa, wa);
+      fetch_w(0, wa);
 #pragma unroll 1
       for (int i = 0; i < MAXCH; i += 2) {
-        fetch(i + 1, xb, wb);
+        fetch_w(i + 1, wb);
         __builtin_amdgcn_sched_barrier(0);
-        step(i, xa, wa);
+        {
+          Raw8<XDT> xa[kTT];
+          fetch_x(i, xa);
+          step(i, xa, wa);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        fetch(i + 2, xa, wa);
+        fetch_w(i + 2, wa);
         __builtin_amdgcn_sched_barrier(0);
-        if (i + 1 < MAXCH) step(i + 1, xb, wb);
+        if (i + 1 < MAXCH) {
+          Raw8<XDT> xa[kTT];
+          fetch_x(i + 1, xa);
+          step(i + 1, xa, wb);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -219,7 +264,8 @@ __global__ __launch_bounds__(NWV * 64) void logits_topk_kernel(RouteArgs a) {
       Raw8<WDT> wa[kEE];
 #pragma unroll 1
       for (int i = 0; i < MAXCH; ++i) {
-        fetch(i, xa, wa);
+        fetch_w(i, wa);
+        fetch_x(i, xa);
         step(i, xa, wa);
       }
     }
