@@ -507,14 +507,21 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
     int n_shared, int bm, int max_tiles, int key_bits, int32_t *counts, int32_t *offsets,
     int32_t *row_token, int32_t *row_pair, int32_t *inv_perm, int32_t *tiles, int32_t *n_tiles) {
   const int lane = lane_id();
-  for (int64_t t = threadIdx.x >> 6; t < T; t += kFusedWaves) {
-    float vals[EREG];
+  // token t + 16's logits are loaded while token t is ranked
+  auto load_row = [&](int64_t t, float (&v)[EREG]) {
 #pragma unroll
     for (int r = 0; r < EREG; ++r) {
       const int e = 64 * r + lane;
-      vals[r] = e < E ? load_as_f32(logits, dtype, t * E + e) : -INFINITY;
+      v[r] = t < T && e < E ? load_as_f32(logits, dtype, t * E + e) : -INFINITY;
     }
-    select_topk<EREG>(vals, E, k, norm, t, idx, w);
+  };
+  float cur[EREG], nxt[EREG];
+  load_row(threadIdx.x >> 6, cur);
+  for (int64_t t = threadIdx.x >> 6; t < T; t += kFusedWaves) {
+    load_row(t + kFusedWaves, nxt);
+    select_topk<EREG>(cur, E, k, norm, t, idx, w);
+#pragma unroll
+    for (int r = 0; r < EREG; ++r) cur[r] = nxt[r];
   }
   __syncthreads();
   permute_block<PPL>(idx, T, k, E, n_shared, bm, max_tiles, key_bits, counts, offsets, row_token, row_pair,
