@@ -86,6 +86,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Sum over the 64 lanes, the same value in every lane: the pairing of
+// wave_max, each level adding two partial sums (commutative, so both lanes
+// of a pair hold the identical result).
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Top-k of the logits held by one wave (expert e = 64 r + lane in vals[r]),
 // ranked by value with ties to the lower index (NaN ranks last); softmax
 // weights over all E experts; optional renormalisation over the selected k.
@@ -115,14 +129,12 @@ __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&ra
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < EREG; ++r) mx = fmaxf(mx, vals[r]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max(mx);
     float den = 0.f;
 #pragma unroll
     for (int r = 0; r < EREG; ++r)
       if (64 * r + lane < E) den += expf(vals[r] - mx);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o);
+    den = wave_sum(den);
 #pragma unroll
     for (int r = 0; r < EREG; ++r)
       vals[r] = 64 * r + lane < E ? round_logit(expf(vals[r] - mx) / den, prob_dtype) : -INFINITY;
@@ -159,8 +171,7 @@ __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&ra
 #pragma unroll
     for (int r = 0; r < EREG; ++r)
       if (64 * r + lane < E && rank[r] < k) psum += vals[r];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) psum += __shfl_xor(psum, o);
+    psum = wave_sum(psum);
     const float s = round_logit(psum, prob_dtype);
 #pragma unroll
     for (int r = 0; r < EREG; ++r) wsel[r] = norm ? round_logit(vals[r] / s, prob_dtype) : vals[r];
@@ -171,8 +182,7 @@ __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&ra
 #pragma unroll
   for (int r = 0; r < EREG; ++r)
     if (64 * r + lane < E) den += __expf(vals[r] - m);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o);
+  den = wave_sum(den);
   float p[EREG];
   float psum = 0.f;
 #pragma unroll
@@ -180,8 +190,7 @@ __device__ void topk_ranks(float (&vals)[EREG], int E, int k, int norm, int (&ra
     p[r] = __expf(vals[r] - m) / den;
     if (64 * r + lane < E && rank[r] < k) psum += p[r];
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) psum += __shfl_xor(psum, o);
+  psum = wave_sum(psum);
 #pragma unroll
   for (int r = 0; r < EREG; ++r) wsel[r] = norm ? p[r] / psum : p[r];
 }
