@@ -174,10 +174,11 @@ static int moe_forward(const moeq_moe *m, const void *x, int64_t T, void *out, i
 
   bool x16_done = false;
   // The fused top-k + permutation work-group ranks its tokens one per wave,
-  // 16 at a time, one after another; past two tokens per wave the top-k of
+  // 16 at a time, one after another; past one token per wave the top-k of
   // every token at once over the GPU plus a separate permutation launch is
-  // faster (Qwen3-shaped, 64 tokens: 22 us fused, about 11 us split).
-  constexpr int64_t kFusedTopkTokens = 32;
+  // faster (Qwen3-shaped, 64 tokens: 22 us fused, about 11 us split; the
+  // OLMoE-shaped 32-token layer 78.7 -> 76.2 us).
+  constexpr int64_t kFusedTopkTokens = 16;
   if (T <= 64 && m->hidden % 8 == 0 && m->hidden <= 4096 &&
       topk_permute_fits(T, m->top_k, m->n_experts, m->n_shared)) {
     // small batches: logits, then top-k and the permutation in one work-group

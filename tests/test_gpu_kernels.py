@@ -93,6 +93,25 @@ def test_route_bit_exact(device, gate, T, H, E, k, norm):
     np.testing.assert_allclose(to_np(w2), ref_w, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("T,H,E,k", [(1, 1024, 64, 6), (300, 1024, 64, 6), (2100, 2560, 8, 2)])
+def test_route_fp32_activations(device, T, H, E, k):
+    """fp32 activations with an fp32 gate, logits kept in fp32: T = 1 through
+    logits_kernel, the others (T * E > 16384) through logits_topk_kernel,
+    which reads fp32 rows straight from global memory (16-bit rows are
+    staged in LDS)."""
+    from robustgemq_amd import ops
+    _say(f"[route] fp32 x T={T} H={H} E={E} k={k}")
+    g = torch.Generator().manual_seed(T * 3 + E)
+    x = torch.randn(T, H, generator=g)
+    wg = torch.randn(E, H, generator=g) * 0.02
+    lg, idx, w = ops.route(x.to(device), wg.to(device), k, True)
+    ref_lg = orr.router_logits(x.numpy(), wg.numpy(), "f32")
+    np.testing.assert_array_equal(lg.float().cpu().numpy().view(np.uint32), ref_lg.view(np.uint32))
+    ref_idx, ref_w = orr.topk_route(ref_lg, k, True)
+    np.testing.assert_array_equal(to_np(idx), ref_idx)
+    np.testing.assert_allclose(to_np(w), ref_w, rtol=2e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("E,k", [(8, 2), (64, 8), (96, 16), (300, 6)])
 def test_topk_special_values_and_ties(device, E, k):
     """Selection order on hand-made logit rows: a stable descending sort
