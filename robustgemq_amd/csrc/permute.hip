@@ -408,6 +408,15 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
   __shared__ int wcnt[4][kFusedExperts];
   const int c = blockIdx.x, e = threadIdx.x, w = e >> 6, lane = lane_id();
   const int Ti = int(T), P = int(T) * k;
+  // this chunk's pairs: wave w takes positions [128 w, 128 w + 128) of it
+  // (loaded first, so their round trip overlaps the chunk counts' and the scan)
+  int ex[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = c * kWgChunk + 128 * w + 64 * j + lane;
+    const int sl = p / Ti, t = p - sl * Ti;
+    ex[j] = p < P ? idx[int64_t(t) * k + sl] : -1;
+  }
   // this expert's rows over all chunks, and over the chunks before this one
   int tot = 0, pre = 0;
   if (e < E) {
@@ -440,16 +449,9 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
     int total;
     off = block_exclusive_scan(e < E + n_shared ? tot : 0, sh, &total);
   }
-  // this chunk's pairs: wave w takes positions [128 w, 128 w + 128) of it
-  int ex[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int p = c * kWgChunk + 128 * w + 64 * j + lane;
-    const int sl = p / Ti, t = p - sl * Ti;
-    const int v = p < P ? idx[int64_t(t) * k + sl] : -1;
-    ex[j] = (v >= 0 && v < E) ? v : -1;
-  }
   for (int i = threadIdx.x; i < 4 * kFusedExperts; i += 256) (&wcnt[0][0])[i] = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) ex[j] = (ex[j] >= 0 && ex[j] < E) ? ex[j] : -1;  // -1: past the end or bad id
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 2; ++j)
