@@ -71,7 +71,8 @@ def test_pack_and_repack_bit_exact(device, nbits):
                                          (2048, 2048, 64, 8, False),
                                          (257, 2048, 128, 8, True), (64, 4096, 8, 2, True),
                                          (40, 1536, 64, 6, False), (16, 512, 8, 2, False),
-                                         (300, 1000, 60, 4, True), (130, 768, 256, 8, False)])
+                                         (300, 1000, 60, 4, True), (130, 768, 256, 8, False),
+                                         (2100, 2560, 8, 2, True)])
 def test_route_bit_exact(device, gate, T, H, E, k, norm):
     from robustgemq_amd import ops
     _say(f"[route] gate={gate} T={T} H={H} E={E} k={k}")
