@@ -323,7 +323,8 @@ static void launch_logits_topk_dt(const RouteArgs &a, int maxch, hipStream_t s) 
   else if (a.E <= 16) launch_logits_topk_nw<XDT, WDT, 2, 8>(a, maxch, s);
   else if (a.E <= 32) launch_logits_topk_nw<XDT, WDT, 4, 8>(a, maxch, s);
   // bf16 with more than 64 experts: four waves per work-group, so the two
-  // work-groups on a CU run out of step (Qwen3 T = 4096: 49.2 -> 46.1 us)
+  // work-groups on a CU run out of step (Qwen3-shaped T = 4096 routing
+  // alone: 49.2 -> 46.1 us)
   else if (XDT == MOEQ_BF16 && a.E > 64) launch_logits_topk_nw<XDT, WDT, 4, 8>(a, maxch, s);
   else launch_logits_topk_nw<XDT, WDT, 8, 8>(a, maxch, s);
 }
